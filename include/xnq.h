@@ -1,0 +1,150 @@
+/*
+ * xnq.h -- C ABI of libxnq, the MI355X (gfx950) GGUF quantized-matmul backend.
+ *
+ * Each entry point replaces one piece of xn's quantized-tensor contract
+ * (gradium-ai/xn, xn-core/src/quantized/mod.rs) with a device-resident
+ * equivalent.  All pointers named *_dev are device (HBM) pointers, all sizes
+ * are element or byte counts, `stream` is a hipStream_t (NULL = the null
+ * stream).  No torch or C++ types cross this boundary.
+ *
+ * Errors: every call returns an xnq_status; on failure a message describing
+ * the problem is available from xnq_last_error() on the calling thread
+ * (mirrors xn's Result<_, Error> + bail!, xn-core/src/error.rs:9-60).
+ *
+ * Threading: a qtensor is read-only after upload, so concurrent matmul calls
+ * on one qtensor from several threads/streams are safe (xn's
+ * `QuantizedType: Send + Sync`, mod.rs:199).
+ */
+#ifndef XNQ_H
+#define XNQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    XNQ_OK = 0,
+    XNQ_ERR_INVALID = 1,     /* shape / size / argument error (xn: bail!) */
+    XNQ_ERR_UNSUPPORTED = 2, /* dtype has no device implementation */
+    XNQ_ERR_HIP = 3,         /* a HIP runtime call failed */
+    XNQ_ERR_OOM = 4          /* device allocation failed */
+} xnq_status;
+
+/* GGML dtype ids, identical to GgmlDType::to_u32 (mod.rs:119-137). */
+enum {
+    XNQ_F32 = 0,
+    XNQ_F16 = 1,
+    XNQ_Q4_0 = 2,
+    XNQ_Q8_0 = 8,
+    XNQ_Q4K = 12,
+    XNQ_Q6K = 14,
+    XNQ_Q8K = 15
+};
+
+typedef struct xnq_qtensor xnq_qtensor;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* xnq_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int xnq_abi_version(void);
+
+/* Bytes per block / elements per block of a GGML dtype, 0 if unknown.
+ * Replaces GgmlDType::type_size / block_size (mod.rs:160-195). */
+size_t xnq_type_size(uint32_t dtype);
+size_t xnq_block_size(uint32_t dtype);
+
+/* Upload a GGUF tensor of n rows x k columns whose canonical block bytes sit
+ * in host memory, and repack it on the device.  Replaces the
+ * `ggml_file::qtensor_from_ggml` -> `QTensor::new(QStorage::Cpu(..))` load
+ * (ggml_file.rs:128-163, mod.rs:32-34) with a device storage; the GGUF bytes
+ * themselves are not changed.  Synchronises `stream` before returning so the
+ * host buffer may be released. */
+xnq_status xnq_qtensor_upload(int device, uint32_t dtype, const void* gguf_blocks_host,
+                              size_t n, size_t k, void* stream, xnq_qtensor** out);
+
+/* As xnq_qtensor_upload, for canonical GGUF block bytes already in device
+ * memory (stream ordered, no synchronisation). */
+xnq_status xnq_qtensor_upload_device(int device, uint32_t dtype, const void* gguf_blocks_dev,
+                                     size_t n, size_t k, void* stream, xnq_qtensor** out);
+
+/* Quantize an n x k f32 weight that lives in device memory.  Replaces
+ * QTensor::quantize_f32 (mod.rs:283-303), i.e. the per-dtype
+ * GgmlType::from_float (k_quants.rs:235-270, 636-661, 1418-1473, 1801-1871);
+ * the blocks produced are byte-identical to the CPU quantizer's. */
+xnq_status xnq_qtensor_quantize(int device, uint32_t dtype, const float* src_dev, size_t n,
+                                size_t k, void* stream, xnq_qtensor** out);
+
+/* Release a qtensor and its device memory (xn: Drop). */
+void xnq_qtensor_free(xnq_qtensor* qt);
+
+/* Introspection (QTensor::dtype / shape / storage_size_in_bytes, mod.rs:305-331).
+ * storage bytes = canonical GGUF size; device bytes = what the repacked copy
+ * occupies in HBM. */
+uint32_t xnq_qtensor_dtype(const xnq_qtensor* qt);
+size_t xnq_qtensor_rows(const xnq_qtensor* qt);
+size_t xnq_qtensor_cols(const xnq_qtensor* qt);
+int xnq_qtensor_device(const xnq_qtensor* qt);
+size_t xnq_qtensor_storage_size(const xnq_qtensor* qt);
+size_t xnq_qtensor_device_bytes(const xnq_qtensor* qt);
+
+/* dst[m x n] = lhs[m x k] . W^T, with lhs quantized to the weight's vec-dot
+ * type first.  Replaces QTensor::matmul_t / QuantizedType::matmul_t /
+ * k_quants::matmul (mod.rs:334-339, 221-223; k_quants.rs:1996-2011).  The
+ * route is chosen from m: a wavefront-per-row matvec for small m, an int8
+ * MFMA kernel for prefill-sized m.  Validates what xn validates:
+ * mkn against the weight shape (repack.rs:203-215) and m*k == lhs length is
+ * the caller's contract.  Stream ordered; allocates its activation scratch
+ * stream-ordered (hipMallocAsync). */
+xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                const float* lhs_dev, float* dst_dev, void* stream);
+
+/* The two halves of matmul_t, for callers that keep the quantized
+ * activation around (k_quants.rs:2014-2026 quantize_lhs, then T::matmul).
+ * The activation workspace layout is private to the library; size it with
+ * xnq_lhs_workspace_size. */
+size_t xnq_lhs_workspace_size(uint32_t weight_dtype, size_t m, size_t k);
+xnq_status xnq_quantize_lhs(uint32_t weight_dtype, size_t m, size_t k, const float* lhs_dev,
+                            void* workspace_dev, void* stream);
+xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                   const void* workspace_dev, float* dst_dev, void* stream);
+
+/* Force a route for matmul_preq (testing and benchmarking): 0 = automatic,
+ * 1 = matvec kernel, 2 = MFMA kernel.  Process wide. */
+xnq_status xnq_set_route(int route);
+
+/* Dequantize into elem_count f32 values (QTensor::dequantize /
+ * GgmlType::to_float, mod.rs:316-318). */
+xnq_status xnq_qtensor_dequantize(const xnq_qtensor* qt, float* dst_dev, size_t elem_count,
+                                  void* stream);
+
+/* Canonical GGUF block bytes of the tensor (QuantizedType::raw_data,
+ * mod.rs:206-214): undoes the device repack.  Copies into host memory and
+ * synchronises. */
+xnq_status xnq_qtensor_raw_data(const xnq_qtensor* qt, void* host_dst, size_t cap, void* stream);
+
+/* Quantize m rows of k f32 activations to canonical BlockQ8_0
+ * (act_dtype = XNQ_Q8_0, k_quants.rs:636-661) or BlockQ8K
+ * (act_dtype = XNQ_Q8K, k_quants.rs:1942-1979) blocks in device memory.
+ * Bit-identical to the CPU quantizer. */
+xnq_status xnq_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const float* src_dev,
+                                   void* blocks_dev, void* stream);
+
+/* Integer parts of every per-block dot product the matvec kernel forms, for
+ * bit-exactness checks against the CPU vec_dot (k_quants.rs:287-304,
+ * 677-691, 1337-1416, 1743-1798).  workspace_dev comes from
+ * xnq_quantize_lhs.  out_dev receives int32 [m][n][k/256 or k/32][2]:
+ *   Q4_0, Q8_0: [block integer sum, 0]
+ *   Q4K:        [sum_j sc_j * sum q4*q8, sum_j m_j * bsum_j]
+ *   Q6K:        [sum_j sc_j * sum (q6-32)*q8, 0] */
+xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* workspace_dev,
+                                  int32_t* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XNQ_H */

@@ -1,0 +1,185 @@
+"""TEST INFRASTRUCTURE ONLY -- the CPU oracle for xn's quantized matmul path.
+
+ctypes wrappers over oracle/build/liboracle.so (xnq_oracle.c: scalar
+restatement of xn-core/src/quantized/k_quants.rs + utils.rs; xnq_cpu_avx2.c:
+the AVX2 baseline restating avx.rs).  Only tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg may import this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "build", "liboracle.so")
+
+Q4_0, Q8_0, Q4K, Q6K, Q8K = 2, 8, 12, 14, 15
+TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292}
+BLOCK_SIZE = {Q4_0: 32, Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-B", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = ctypes.CDLL(LIB)
+        sz, vp, i = ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        for name in ("orc_from_float", "orc_to_float"):
+            getattr(L, name).restype = i
+            getattr(L, name).argtypes = [i, vp, vp, sz]
+        L.orc_vec_dot.restype = ctypes.c_float
+        L.orc_vec_dot.argtypes = [i, sz, vp, vp]
+        L.orc_quantize_lhs.restype = i
+        L.orc_quantize_lhs.argtypes = [i, sz, sz, vp, vp]
+        L.orc_matmul_preq.restype = i
+        L.orc_matmul_preq.argtypes = [i, sz, sz, sz, vp, vp, vp]
+        L.orc_matmul.restype = i
+        L.orc_matmul.argtypes = [i, sz, sz, sz, vp, vp, vp]
+        L.orc_q4k_block_ints.argtypes = [vp, vp, vp]
+        L.orc_q6k_block_ints.argtypes = [vp, vp, vp]
+        L.orc_get_scale_min_k4.argtypes = [i, vp, vp]
+        L.orc_q4k_unpack_scales_kmask.argtypes = [vp, vp, vp]
+        L.orc_make_qkx1_quants.restype = ctypes.c_float
+        L.orc_make_qkx1_quants.argtypes = [i, i, vp, i, vp]
+        L.orc_make_qx_quants.restype = ctypes.c_float
+        L.orc_make_qx_quants.argtypes = [i, i, vp, vp, i]
+        L.cpu_pool_init.restype = i
+        L.cpu_pool_init.argtypes = [sz]
+        L.cpu_matmul.restype = i
+        L.cpu_matmul.argtypes = [i, sz, sz, sz, vp, vp, vp, vp]
+        L.cpu_matmul_preq.restype = i
+        L.cpu_matmul_preq.argtypes = [i, sz, sz, sz, vp, vp, vp]
+        for name in ("cpu_vec_dot_q4_0", "cpu_vec_dot_q8_0", "cpu_vec_dot_q4k", "cpu_vec_dot_q6k"):
+            getattr(L, name).restype = ctypes.c_float
+            getattr(L, name).argtypes = [sz, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def nbytes(dt: int, nelem: int) -> int:
+    return nelem // BLOCK_SIZE[dt] * TYPE_SIZE[dt]
+
+
+def vec_dot_type(dt: int) -> int:
+    return Q8_0 if dt in (Q4_0, Q8_0) else Q8K
+
+
+def from_float(dt: int, x) -> np.ndarray:
+    """GgmlType::from_float -> canonical block bytes (uint8)."""
+    x = _f32(x).reshape(-1)
+    out = np.zeros(nbytes(dt, x.size), dtype=np.uint8)
+    assert lib().orc_from_float(dt, x.ctypes.data, out.ctypes.data, x.size // BLOCK_SIZE[dt]) == 0
+    return out
+
+
+def to_float(dt: int, blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    nb = blocks.size // TYPE_SIZE[dt]
+    out = np.zeros(nb * BLOCK_SIZE[dt], dtype=np.float32)
+    assert lib().orc_to_float(dt, blocks.ctypes.data, out.ctypes.data, nb) == 0
+    return out
+
+
+def vec_dot(dt: int, k: int, w_row: np.ndarray, a_row: np.ndarray) -> float:
+    return lib().orc_vec_dot(dt, k, w_row.ctypes.data, a_row.ctypes.data)
+
+
+def quantize_lhs(dt: int, lhs) -> np.ndarray:
+    lhs = _f32(lhs)
+    m, k = lhs.shape
+    vt = vec_dot_type(dt)
+    out = np.zeros(m * nbytes(vt, k), dtype=np.uint8)
+    assert lib().orc_quantize_lhs(dt, m, k, lhs.ctypes.data, out.ctypes.data) == 0
+    return out
+
+
+def matmul(dt: int, lhs, w_blocks: np.ndarray, n: int) -> np.ndarray:
+    """k_quants::matmul: (m, k) f32 x W[n, k]^T -> (m, n) f32 (scalar vec_dot_unopt path)."""
+    lhs = _f32(lhs)
+    m, k = lhs.shape
+    w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    dst = np.zeros((m, n), dtype=np.float32)
+    assert lib().orc_matmul(dt, m, k, n, lhs.ctypes.data, w_blocks.ctypes.data, dst.ctypes.data) == 0
+    return dst
+
+
+def matmul_preq(dt: int, lhs_blocks: np.ndarray, w_blocks: np.ndarray, m: int, k: int, n: int) -> np.ndarray:
+    dst = np.zeros((m, n), dtype=np.float32)
+    assert lib().orc_matmul_preq(dt, m, k, n, lhs_blocks.ctypes.data, w_blocks.ctypes.data,
+                                 dst.ctypes.data) == 0
+    return dst
+
+
+def block_ints(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: int, k: int) -> np.ndarray:
+    """int64 [m, n, nb, 2]: the integer parts of every block dot, as the CPU
+    vec_dot forms them (see orc_q4k_block_ints / orc_q6k_block_ints)."""
+    bs = BLOCK_SIZE[dt]
+    nb = k // bs
+    vt = vec_dot_type(dt)
+    out = np.zeros((m, n, nb, 2), dtype=np.int64)
+    wv = w_blocks.reshape(n, nb, TYPE_SIZE[dt])
+    if dt in (Q4K, Q6K):
+        av = a_blocks.reshape(m, nb, TYPE_SIZE[vt])
+        fn = lib().orc_q4k_block_ints if dt == Q4K else lib().orc_q6k_block_ints
+        tmp = np.zeros(2, dtype=np.int64)
+        for r in range(m):
+            for c in range(n):
+                for b in range(nb):
+                    wb = np.ascontiguousarray(wv[c, b])
+                    ab = np.ascontiguousarray(av[r, b])
+                    tmp[:] = 0
+                    fn(wb.ctypes.data, ab.ctypes.data, tmp.ctypes.data)
+                    out[r, c, b] = tmp
+        return out
+    # Q4_0 / Q8_0: integer block sums, vectorised
+    av = a_blocks.reshape(m, nb, 34)
+    aq = av[:, :, 2:].view(np.int8).astype(np.int64)  # [m, nb, 32]
+    if dt == Q8_0:
+        wq = wv[:, :, 2:].view(np.int8).astype(np.int64)
+    else:
+        qs = wv[:, :, 2:].astype(np.int64)
+        wq = np.concatenate([(qs & 0xF) - 8, (qs >> 4) - 8], axis=2)
+    out[..., 0] = np.einsum("mbe,nbe->mnb", aq, wq)
+    return out
+
+
+def cpu_pool_init(threads: int) -> int:
+    return lib().cpu_pool_init(threads)
+
+
+def cpu_matmul(dt: int, lhs: np.ndarray, w_blocks: np.ndarray, n: int, scratch: np.ndarray | None = None) -> np.ndarray:
+    """The AVX2 baseline: serial quantize_lhs then the threaded kernel."""
+    lhs = _f32(lhs)
+    m, k = lhs.shape
+    if scratch is None:
+        scratch = np.zeros(m * nbytes(vec_dot_type(dt), k), dtype=np.uint8)
+    dst = np.zeros((m, n), dtype=np.float32)
+    assert lib().cpu_matmul(dt, m, k, n, lhs.ctypes.data, w_blocks.ctypes.data, dst.ctypes.data,
+                            scratch.ctypes.data) == 0
+    return dst
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return lib().orc_f32_to_f16(x)
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return lib().orc_f16_to_f32(h)

@@ -1,0 +1,176 @@
+"""Independent numpy codecs of the GGUF block formats, written from the format
+description (k_quants.rs:92-205 struct layouts; the bit layouts of
+utils.rs:53-63 and k_quants.rs:1759-1771), used to check the oracle and the
+device kernels from a second direction: these pack known integers into
+bytes and unpack bytes into integers, whereas the oracle quantizes floats.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F16 = np.float16
+
+
+def _f16_from_bits(b: np.ndarray) -> np.ndarray:
+    return np.asarray(b, dtype=np.uint16).view(F16).astype(np.float32)
+
+
+# ----------------------------------------------------------------- Q8_0
+def decode_q8_0(blocks: np.ndarray):
+    """-> d f32 [nb], q int64 [nb, 32]"""
+    b = blocks.reshape(-1, 34)
+    d = _f16_from_bits(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    q = b[:, 2:].view(np.int8).astype(np.int64)
+    return d, q
+
+
+# ----------------------------------------------------------------- Q4_0
+def decode_q4_0(blocks: np.ndarray):
+    """-> d f32 [nb], q int64 [nb, 32] in -8..7"""
+    b = blocks.reshape(-1, 18)
+    d = _f16_from_bits(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    qs = b[:, 2:].astype(np.int64)
+    q = np.concatenate([(qs & 0xF) - 8, (qs >> 4) - 8], axis=1)
+    return d, q
+
+
+# ----------------------------------------------------------------- Q8_K
+def decode_q8k(blocks: np.ndarray):
+    """-> d f32 [nb], q int64 [nb, 256], bsums int64 [nb, 16]"""
+    b = blocks.reshape(-1, 292)
+    d = b[:, 0:4].copy().view(np.float32)[:, 0]
+    q = b[:, 4:260].view(np.int8).astype(np.int64)
+    bs = b[:, 260:292].copy().view(np.int16).astype(np.int64)
+    return d, q, bs
+
+
+# ----------------------------------------------------------------- Q4_K
+def pack_scales_k4(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """8 six-bit scales and mins -> the 12 packed bytes.
+    Bytes 0-3: sc[0..4] low 6 bits, top 2 bits carry sc[4..8] >> 4.
+    Bytes 4-7: mn[0..4] low 6 bits, top 2 bits carry mn[4..8] >> 4.
+    Bytes 8-11: low nibble sc[4..8] & 15, high nibble mn[4..8] & 15."""
+    out = np.zeros(12, dtype=np.uint8)
+    for j in range(4):
+        out[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        out[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        out[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    return out
+
+
+def unpack_scales_k4(b12: np.ndarray):
+    sc = np.zeros(8, dtype=np.int64)
+    mn = np.zeros(8, dtype=np.int64)
+    b = b12.astype(np.int64)
+    for j in range(4):
+        sc[j] = b[j] & 63
+        mn[j] = b[j + 4] & 63
+        sc[j + 4] = (b[j + 8] & 15) | ((b[j] >> 6) << 4)
+        mn[j + 4] = (b[j + 8] >> 4) | ((b[j + 4] >> 6) << 4)
+    return sc, mn
+
+
+def encode_q4k(d_bits: int, dmin_bits: int, sc, mn, q) -> np.ndarray:
+    """One BlockQ4K from integer fields: q[256] in 0..15 in element order.
+    qs byte 32*p + l holds element 64p+l (low nibble) and 64p+32+l (high)."""
+    q = np.asarray(q, dtype=np.int64)
+    out = np.zeros(144, dtype=np.uint8)
+    out[0:2] = np.array([d_bits], dtype=np.uint16).view(np.uint8)
+    out[2:4] = np.array([dmin_bits], dtype=np.uint16).view(np.uint8)
+    out[4:16] = pack_scales_k4(np.asarray(sc, np.int64), np.asarray(mn, np.int64))
+    for p in range(4):
+        for l in range(32):
+            out[16 + 32 * p + l] = q[64 * p + l] | (q[64 * p + 32 + l] << 4)
+    return out
+
+
+def decode_q4k(blocks: np.ndarray):
+    """-> d, dmin f32 [nb]; sc, mn int64 [nb, 8]; q int64 [nb, 256] in 0..15"""
+    b = blocks.reshape(-1, 144)
+    nb = b.shape[0]
+    d = _f16_from_bits(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    dmin = _f16_from_bits(b[:, 2:4].copy().view(np.uint16)[:, 0])
+    sc = np.zeros((nb, 8), np.int64)
+    mn = np.zeros((nb, 8), np.int64)
+    for i in range(nb):
+        sc[i], mn[i] = unpack_scales_k4(b[i, 4:16])
+    qs = b[:, 16:].astype(np.int64).reshape(nb, 4, 32)
+    q = np.concatenate([np.stack([qs[:, p] & 0xF, qs[:, p] >> 4], axis=1) for p in range(4)], axis=1)
+    return d, dmin, sc, mn, q.reshape(nb, 256)
+
+
+# ----------------------------------------------------------------- Q6_K
+def encode_q6k(d_bits: int, sc, q) -> np.ndarray:
+    """One BlockQ6K: q[256] in 0..63 (value + 32), sc[16] int8.
+    For half h, l < 32: ql[64h+l] = q(128h+l) | q(128h+64+l) << 4 (low 4 bits),
+    ql[64h+32+l] = q(128h+32+l) | q(128h+96+l) << 4, qh[32h+l] packs the top
+    2 bits of q(128h+l), q(+32), q(+64), q(+96) at bits 0, 2, 4, 6."""
+    q = np.asarray(q, dtype=np.int64)
+    out = np.zeros(210, dtype=np.uint8)
+    for h in range(2):
+        for l in range(32):
+            e = 128 * h + l
+            out[64 * h + l] = (q[e] & 15) | ((q[e + 64] & 15) << 4)
+            out[64 * h + 32 + l] = (q[e + 32] & 15) | ((q[e + 96] & 15) << 4)
+            out[128 + 32 * h + l] = (q[e] >> 4) | ((q[e + 32] >> 4) << 2) | ((q[e + 64] >> 4) << 4) | (
+                (q[e + 96] >> 4) << 6)
+    out[192:208] = np.asarray(sc, dtype=np.int8).view(np.uint8)
+    out[208:210] = np.array([d_bits], dtype=np.uint16).view(np.uint8)
+    return out
+
+
+def decode_q6k(blocks: np.ndarray):
+    """-> d f32 [nb], sc int64 [nb, 16], q int64 [nb, 256] in -32..31"""
+    b = blocks.reshape(-1, 210)
+    nb = b.shape[0]
+    ql = b[:, :128].astype(np.int64)
+    qh = b[:, 128:192].astype(np.int64)
+    sc = b[:, 192:208].view(np.int8).astype(np.int64)
+    d = _f16_from_bits(b[:, 208:210].copy().view(np.uint16)[:, 0])
+    q = np.zeros((nb, 256), np.int64)
+    for h in range(2):
+        for l in range(32):
+            e = 128 * h + l
+            lo0, lo1 = ql[:, 64 * h + l], ql[:, 64 * h + 32 + l]
+            hb = qh[:, 32 * h + l]
+            q[:, e] = (lo0 & 15) | ((hb & 3) << 4)
+            q[:, e + 32] = (lo1 & 15) | (((hb >> 2) & 3) << 4)
+            q[:, e + 64] = (lo0 >> 4) | (((hb >> 4) & 3) << 4)
+            q[:, e + 96] = (lo1 >> 4) | (((hb >> 6) & 3) << 4)
+    return d, sc, q - 32
+
+
+# ------------------------------------------------- brute-force integer dots
+def block_ints_bruteforce(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: int, k: int):
+    """int64 [m, n, nb, 2] from decoded integers (see xnq.h block_ints)."""
+    if dt in (2, 8):
+        nb = k // 32
+        da, qa = decode_q8_0(a_blocks)
+        qa = qa.reshape(m, nb, 32)
+        _, qw = (decode_q8_0 if dt == 8 else decode_q4_0)(w_blocks)
+        qw = qw.reshape(n, nb, 32)
+        out = np.zeros((m, n, nb, 2), np.int64)
+        out[..., 0] = np.einsum("mbe,nbe->mnb", qa, qw)
+        return out
+    nb = k // 256
+    _, qa, bsums = decode_q8k(a_blocks)
+    qa = qa.reshape(m, nb, 256)
+    out = np.zeros((m, n, nb, 2), np.int64)
+    if dt == 12:
+        _, _, sc, mn, q = decode_q4k(w_blocks)
+        sc = sc.reshape(n, nb, 8)
+        mn = mn.reshape(n, nb, 8)
+        q = q.reshape(n, nb, 8, 32)
+        qa8 = qa.reshape(m, nb, 8, 32)
+        sub = np.einsum("mbje,nbje->mnbj", qa8, q)  # per sub-block integer dots
+        out[..., 0] = np.einsum("mnbj,nbj->mnb", sub, sc)
+        s32 = qa8.sum(axis=3)  # [m, nb, 8]
+        out[..., 1] = np.einsum("mbj,nbj->mnb", s32, mn)
+    else:
+        _, sc, q = decode_q6k(w_blocks)
+        sc = sc.reshape(n, nb, 16)
+        q = q.reshape(n, nb, 16, 16)
+        qa16 = qa.reshape(m, nb, 16, 16)
+        sub = np.einsum("mbje,nbje->mnbj", qa16, q)
+        out[..., 0] = np.einsum("mnbj,nbj->mnb", sub, sc)
+    return out

@@ -1,0 +1,224 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (from the path's contract):
+  * activation quantization (Q8_0, Q8_K), weight quantization, repack round
+    trips, dequantization and per-block integer dots: bit-exact;
+  * f32 matmul outputs: relative L2 <= 1e-3 and, per output row,
+    max |got - want| / max |want| <= 2e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests import _formats as F
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4K, Q6K, Q8K = 2, 8, 12, 14, 15
+WEIGHT_DTYPES = [Q4_0, Q8_0, Q4K, Q6K]
+REL_L2 = 1e-3
+ROW_MAX_REL = 2e-3
+
+
+def assert_close(got: np.ndarray, want: np.ndarray, what: str = "") -> None:
+    got = got.reshape(want.shape).astype(np.float64)
+    want = want.astype(np.float64)
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    assert rel <= REL_L2, f"{what}: relative L2 {rel:.3e}"
+    w2 = want.reshape(-1, want.shape[-1])
+    g2 = got.reshape(-1, want.shape[-1])
+    row = np.abs(g2 - w2).max(axis=1) / np.maximum(np.abs(w2).max(axis=1), 1e-30)
+    assert row.max() <= ROW_MAX_REL, f"{what}: row max relative error {row.max():.3e} (row {row.argmax()})"
+
+
+def upload(orc_blocks: np.ndarray, n: int, k: int, dt: int, dev):
+    from xn_amd import GgmlDType, QTensor
+
+    return QTensor.from_gguf_bytes(orc_blocks, (n, k), GgmlDType(dt), dev)
+
+
+# ------------------------------------------------- activation quantizers
+@pytest.mark.parametrize("act", [Q8_0, Q8K])
+@pytest.mark.parametrize("m,k", [(1, 256), (3, 4096), (8, 14336), (33, 512)])
+def test_act_quantizer_bit_exact(orc, dev, act, m, k):
+    from xn_amd.quantized import quantize_act_blocks
+
+    rng = np.random.default_rng(1000 + m + act)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    x[0, :256] = 0.0  # an all-zero block
+    if k >= 512:
+        x[-1, 256:512] = rng.normal(0, 1e-30, 256).astype(np.float32)  # tiny values, subnormal scales
+        x[-1, 300], x[-1, 301] = -3.5, 3.5  # tie on |x|: first wins
+    want = orc.from_float(act, x)
+    got = quantize_act_blocks(act, torch.from_numpy(x).to(dev), m, k).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+def test_act_quantizer_edge_values(orc, dev):
+    from xn_amd.quantized import quantize_act_blocks
+
+    rng = np.random.default_rng(7)
+    k = 256
+    rows = [
+        np.full(k, 1.0, np.float32),
+        np.full(k, -2.5, np.float32),
+        np.where(np.arange(k) % 2 == 0, 1e4, -1e4).astype(np.float32),
+        (np.arange(k, dtype=np.float32) - 128) * np.float32(0.5),  # exact halves -> round away from 0
+        rng.normal(0, 1e6, k).astype(np.float32),
+        rng.normal(0, 1e-6, k).astype(np.float32),
+    ]
+    x = np.stack(rows)
+    for act in (Q8_0, Q8K):
+        want = orc.from_float(act, x)
+        got = quantize_act_blocks(act, torch.from_numpy(x).to(dev), x.shape[0], k).cpu().numpy()
+        assert np.array_equal(got, want), f"act dtype {act}"
+
+
+# ------------------------------------------- weight storage round trips
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+def test_upload_raw_data_round_trip(orc, dev, dt):
+    rng = np.random.default_rng(2000 + dt)
+    n, k = 37, 1024
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    qt = upload(blocks, n, k, dt, dev)
+    assert qt.storage_size_in_bytes() == blocks.size
+    assert qt.data() == blocks.tobytes()
+
+
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
+def test_raw_data_round_trip_random_bytes(orc, dev, dt):
+    """Any byte pattern survives repack -> unrepack (the repack is a bijection)."""
+    rng = np.random.default_rng(2100 + dt)
+    n, k = 5, 768
+    blocks = rng.integers(0, 256, n * (k // 256) * orc.TYPE_SIZE[dt]).astype(np.uint8)
+    qt = upload(blocks, n, k, dt, dev)
+    assert qt.data() == blocks.tobytes()
+
+
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+def test_dequantize_bit_exact(orc, dev, dt):
+    rng = np.random.default_rng(3000 + dt)
+    n, k = 19, 1536
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    qt = upload(blocks, n, k, dt, dev)
+    got = qt.dequantize().cpu().numpy().reshape(-1)
+    want = orc.to_float(dt, blocks)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+def test_device_weight_quantizer_bit_exact(orc, dev, dt):
+    from xn_amd import GgmlDType, QTensor
+
+    rng = np.random.default_rng(4000 + dt)
+    n, k = 24, 2048
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    w[1] = 0.0
+    w[2] = 0.125
+    w[3, :256] = np.linspace(-1, 1, 256, dtype=np.float32)
+    qt = QTensor.quantize_f32(torch.from_numpy(w).to(dev), (n, k), GgmlDType(dt))
+    assert qt.data() == orc.from_float(dt, w).tobytes()
+
+
+# ----------------------------------------------------- integer block dots
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+def test_block_ints_bit_exact(orc, dev, dt):
+    from xn_amd.quantized import block_ints, lhs_workspace, quantize_lhs
+
+    rng = np.random.default_rng(5000 + dt)
+    m, n, k = 3, 21, 1024
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    ws = lhs_workspace(qt.dtype(), m, k, dev)
+    quantize_lhs(qt.dtype(), torch.from_numpy(x).to(dev), ws, m, k)
+    got = block_ints(qt, m, ws).cpu().numpy().astype(np.int64)
+    want = F.block_ints_bruteforce(dt, blocks, orc.quantize_lhs(dt, x), m, n, k)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- matmul
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 17])
+def test_matmul_small(orc, dev, dt, m):
+    rng = np.random.default_rng(6000 + 31 * dt + m)
+    n, k = 300, 2048
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m}")
+
+
+@pytest.mark.parametrize("dt,k,n", [
+    (Q8_0, 4096, 4096),   # config 1
+    (Q4_0, 4096, 14336),  # config 2 gate/up
+    (Q4_0, 14336, 4096),  # config 2 down
+    (Q4K, 4096, 4096),    # config 3
+    (Q4K, 4096, 14336),
+    (Q4K, 14336, 4096),
+    (Q6K, 14336, 4096),   # config 5 FFN down
+])
+@pytest.mark.parametrize("m", [1, 4])
+def test_matmul_config_shapes(orc, dev, dt, k, n, m):
+    rng = np.random.default_rng(7000 + dt + k + n + m)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    blocks = orc.from_float(dt, w)
+    del w
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} k={k} n={n} m={m}")
+
+
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
+@pytest.mark.parametrize("m", [64, 130])
+def test_matmul_prefill_sizes(orc, dev, dt, m):
+    rng = np.random.default_rng(8000 + dt + m)
+    n, k = 512, 4096
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m}")
+
+
+def test_qlinear_vs_linear(dev):
+    """tests/quantized_tests.rs:14-118: QLinear(Q8_0) vs f32 Linear, 64->32,
+    batch 4 (and 2x3 3-D input), max error < 0.3, with and without bias."""
+    from xn_amd import GgmlDType, QLinear
+
+    g = torch.Generator().manual_seed(299792458)
+    w = torch.randn(32, 64, generator=g)
+    b = torch.randn(32, generator=g)
+    for xs in (torch.randn(4, 64, generator=g), torch.randn(2, 3, 64, generator=g)):
+        for bias in (None, b):
+            ref = xs @ w.T + (0 if bias is None else bias)
+            ql = QLinear.from_linear(w.to(dev), None if bias is None else bias.to(dev), GgmlDType.Q8_0)
+            out = ql.forward(xs.to(dev)).cpu()
+            assert out.shape == ref.shape
+            assert (out - ref).abs().max().item() < 0.3
+
+
+# ------------------------------------------------------------ error paths
+def test_errors(orc, dev):
+    from xn_amd import GgmlDType, QTensor, XnqError
+
+    rng = np.random.default_rng(9)
+    blocks = orc.from_float(Q4K, rng.normal(0, 0.02, (4, 256)))
+    with pytest.raises(XnqError, match="divisible"):
+        QTensor.from_gguf_bytes(blocks, (8, 128), GgmlDType.Q4K, dev)
+    with pytest.raises(XnqError, match="not supported"):
+        QTensor.from_gguf_bytes(np.zeros(84, np.uint8), (1, 256), GgmlDType.Q2K, dev)
+    qt = QTensor.from_gguf_bytes(blocks, (4, 256), GgmlDType.Q4K, dev)
+    lhs = torch.zeros(512, device=dev)
+    dst = torch.zeros(8, device=dev)
+    with pytest.raises(XnqError, match="does not match"):
+        qt.matmul_t((1, 512, 4), lhs, dst)
+    with pytest.raises(XnqError, match="unexpected lhs length"):
+        qt.matmul_t((2, 256, 4), lhs[:100], dst)
+    # m = 0 is a no-op
+    qt.matmul_t((0, 256, 4), lhs[:0], dst[:0])

@@ -1,0 +1,493 @@
+// Quantizers on the device, bit-identical to xn's CPU quantizers:
+//   * activations ("lhs") to Q8_0 / Q8_K, into the private planar workspace
+//     used by the matmul kernels or into canonical GGUF blocks;
+//   * weights (QTensor::quantize_f32) to Q8_0 / Q4_0 / Q4_K / Q6_K GGUF blocks.
+// No multiply-add is fused in this file, so every f32 operation rounds exactly
+// where the reference's does.
+#pragma clang fp contract(off)
+
+#include "xnq_device.h"
+#include "xnq_internal.h"
+
+namespace xnq {
+
+namespace {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Q8_K activations, k_quants.rs:1942-1979.  One wavefront per 256-element
+// block, four consecutive elements per lane.
+// ---------------------------------------------------------------------------
+template <bool CANONICAL>
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
+                                                            size_t nblocks, size_t blocks_per_row,
+                                                            int8_t* __restrict__ q,
+                                                            float* __restrict__ dplane,
+                                                            int16_t* __restrict__ splane,
+                                                            uint8_t* __restrict__ canon) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const size_t blk = (size_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+    if (blk >= nblocks) return;
+    const float4 v = reinterpret_cast<const float4*>(x + blk * 256)[lane];
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+
+    // Largest |x|, first index on ties (the reference's strict `amax < |x|`).
+    float amax = 0.0f;
+    int idx = 0x7fffffff;
+    float max = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a = fabsf(xs[i]);
+        if (amax < a) {
+            amax = a;
+            max = xs[i];
+            idx = lane * 4 + i;
+        }
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        float oa = __shfl_xor(amax, off);
+        int oi = __shfl_xor(idx, off);
+        float om = __shfl_xor(max, off);
+        bool take = (oa > amax) || (oa == amax && oi < idx);
+        if (take) {
+            amax = oa;
+            idx = oi;
+            max = om;
+        }
+    }
+
+    int8_t qv[4];
+    float d;
+    if (amax == 0.0f) {
+        qv[0] = qv[1] = qv[2] = qv[3] = 0;
+        d = 0.0f;
+    } else {
+        const float iscale = -128.0f / max;
+#pragma unroll
+        for (int i = 0; i < 4; i++) qv[i] = f_as_i8(fminf(roundf(iscale * xs[i]), 127.0f));
+        d = 1.0f / iscale;
+    }
+    int s = (int)qv[0] + qv[1] + qv[2] + qv[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    const uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
+                            ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
+    if (CANONICAL) {
+        // BlockQ8K: f32 d; i8 qs[256]; i16 bsums[16]  (292 bytes, 4-byte aligned)
+        uint8_t* b = canon + blk * 292;
+        reinterpret_cast<uint32_t*>(b + 4)[lane] = packed;
+        if (lane == 0) *reinterpret_cast<float*>(b) = d;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(b + 260)[lane >> 2] = (int16_t)s;
+    } else {
+        reinterpret_cast<uint32_t*>(q + blk * 256)[lane] = packed;
+        const size_t row = blk / blocks_per_row, b = blk % blocks_per_row;
+        if (lane == 0) dplane[row * blocks_per_row + b] = d;
+        if ((lane & 3) == 0) splane[(row * blocks_per_row + b) * 16 + (lane >> 2)] = (int16_t)s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 activations, k_quants.rs:636-661.  Eight lanes per 32-element block.
+// ---------------------------------------------------------------------------
+template <bool CANONICAL>
+__global__ __launch_bounds__(256) void quantize_q80_kernel(const float* __restrict__ x,
+                                                            size_t nblocks,
+                                                            int8_t* __restrict__ q,
+                                                            uint16_t* __restrict__ dplane,
+                                                            int16_t* __restrict__ splane,
+                                                            uint8_t* __restrict__ canon) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t blk = t / 8;
+    const int sub = (int)(t & 7);
+    const bool live = blk < nblocks;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) v = reinterpret_cast<const float4*>(x + blk * 32)[sub];
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, 0.0f);
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int8_t q0 = f_as_i8(roundf(v.x * id)), q1 = f_as_i8(roundf(v.y * id)),
+                 q2 = f_as_i8(roundf(v.z * id)), q3 = f_as_i8(roundf(v.w * id));
+    int s = (int)q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (!live) return;
+    const uint16_t dh = f32_to_f16_bits(d);
+    if (CANONICAL) {
+        // BlockQ8_0: f16 d; i8 qs[32]  (34 bytes, 2-byte aligned)
+        uint8_t* b = canon + blk * 34;
+        uint16_t* w = reinterpret_cast<uint16_t*>(b + 2 + 4 * sub);
+        w[0] = (uint16_t)((uint8_t)q0 | ((uint16_t)(uint8_t)q1 << 8));
+        w[1] = (uint16_t)((uint8_t)q2 | ((uint16_t)(uint8_t)q3 << 8));
+        if (sub == 0) *reinterpret_cast<uint16_t*>(b) = dh;
+    } else {
+        const uint32_t packed = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
+                                ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
+        reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = packed;
+        if (sub == 0) {
+            dplane[blk] = dh;
+            splane[blk] = (int16_t)s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight quantizers (one thread per GGUF block), restating the CPU code path
+// of QTensor::quantize_f32.
+// ---------------------------------------------------------------------------
+
+// k_quants.rs:636-661
+__global__ void w_q80_kernel(const float* __restrict__ x, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float* xs = x + i * 32;
+    uint8_t* b = out + i * 34;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(xs[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f32_to_f16_bits(d);
+    b[0] = (uint8_t)dh;
+    b[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 32; j++) b[2 + j] = (uint8_t)f_as_i8(roundf(xs[j] * id));
+}
+
+// k_quants.rs:235-270
+__global__ void w_q40_kernel(const float* __restrict__ x, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float* xs = x + i * 32;
+    uint8_t* b = out + i * 18;
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        if (amax < fabsf(xs[j])) {
+            amax = fabsf(xs[j]);
+            max = xs[j];
+        }
+    }
+    const float d = max / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f32_to_f16_bits(d);
+    b[0] = (uint8_t)dh;
+    b[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 16; j++) {
+        const float x0 = xs[j] * id;
+        const float x1 = xs[16 + j] * id;
+        uint8_t xi0 = f_as_u8(x0 + 8.5f);
+        uint8_t xi1 = f_as_u8(x1 + 8.5f);
+        if (xi0 > 15) xi0 = 15;
+        if (xi1 > 15) xi1 = 15;
+        b[2 + j] = (uint8_t)(xi0 | (xi1 << 4));
+    }
+}
+
+// Rust's f32::total_cmp order as an integer key.
+__device__ __forceinline__ int32_t total_key(float f) {
+    int32_t i = __builtin_bit_cast(int32_t, f);
+    return i ^ (int32_t)(((uint32_t)(i >> 31)) >> 1);
+}
+
+// utils.rs:205-254 make_qkx1_quants(nmax, ntry, x[0..32]); returns scale, -min.
+__device__ float make_qkx1_quants32(int nmax, int ntry, const float* x, float* neg_min) {
+    uint8_t l[32];
+    for (int i = 0; i < 32; i++) l[i] = 0;
+    float mn = x[0], mx = x[0];
+    for (int i = 1; i < 32; i++) {
+        if (total_key(x[i]) < total_key(mn)) mn = x[i];
+        if (total_key(x[i]) >= total_key(mx)) mx = x[i];
+    }
+    if (mx == mn) {
+        *neg_min = 0.0f;
+        return 0.0f;
+    }
+    float min = fminf(mn, 0.0f);
+    float iscale = (float)nmax / (mx - min);
+    float scale = 1.0f / iscale;
+    for (int t = 0; t < ntry; t++) {
+        float sumlx = 0.0f;
+        int32_t suml2 = 0;
+        bool did_change = false;
+        for (int i = 0; i < 32; i++) {
+            const float value = x[i];
+            const int32_t li = clampi(nearest_int(iscale * (value - min)), 0, nmax);
+            const uint8_t cl = (uint8_t)li;
+            if (cl != l[i]) {
+                l[i] = cl;
+                did_change = true;
+            }
+            sumlx += (value - min) * (float)li;
+            suml2 += li * li;
+        }
+        scale = sumlx / (float)suml2;
+        float sum = -0.0f;
+        for (int i = 0; i < 32; i++) sum += x[i] - scale * (float)l[i];
+        min = sum / 32.0f;
+        if (min > 0.0f) min = 0.0f;
+        iscale = 1.0f / scale;
+        if (!did_change) break;
+    }
+    *neg_min = -min;
+    return scale;
+}
+
+__device__ __forceinline__ void get_scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+// k_quants.rs:1418-1473
+__global__ void w_q4k_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t bi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (bi >= nblocks) return;
+    const float* x = xin + bi * 256;
+    uint8_t sc12[12];
+    for (int i = 0; i < 12; i++) sc12[i] = 0;
+    float mins[8], scales[8];
+    for (int j = 0; j < 8; j++) scales[j] = make_qkx1_quants32(15, 5, x + 32 * j, &mins[j]);
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        max_scale = fmaxf(scales[j], max_scale);
+        max_min = fmaxf(mins[j], max_min);
+    }
+    const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    for (int j = 0; j < 8; j++) {
+        int32_t a = nearest_int(inv_scale * scales[j]);
+        if (a > 63) a = 63;
+        int32_t b = nearest_int(inv_min * mins[j]);
+        if (b > 63) b = 63;
+        const uint8_t ls = (uint8_t)a, lm = (uint8_t)b;
+        if (j < 4) {
+            sc12[j] = ls;
+            sc12[j + 4] = lm;
+        } else {
+            sc12[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            sc12[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            sc12[j] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    const uint16_t dh = f32_to_f16_bits(max_scale / 63.0f);
+    const uint16_t mh = f32_to_f16_bits(max_min / 63.0f);
+    uint8_t* blk = out + bi * 144;
+    blk[0] = (uint8_t)dh;
+    blk[1] = (uint8_t)(dh >> 8);
+    blk[2] = (uint8_t)mh;
+    blk[3] = (uint8_t)(mh >> 8);
+    for (int i = 0; i < 12; i++) blk[4 + i] = sc12[i];
+    const float df = f16_bits_to_f32(dh), mf = f16_bits_to_f32(mh);
+    // Quantize one 64-element half-pair at a time and pack straight into qs.
+    for (int p = 0; p < 4; p++) {
+        uint8_t sc0, m0, sc1, m1;
+        get_scale_min_k4(2 * p, sc12, &sc0, &m0);
+        get_scale_min_k4(2 * p + 1, sc12, &sc1, &m1);
+        const float d0 = df * (float)sc0, d1 = df * (float)sc1;
+        const float dm0 = mf * (float)m0, dm1 = mf * (float)m1;
+        for (int lv = 0; lv < 32; lv++) {
+            uint8_t lo = 0, hi = 0;
+            if (d0 != 0.0f) lo = (uint8_t)clampi(nearest_int((x[64 * p + lv] + dm0) / d0), 0, 15);
+            if (d1 != 0.0f) hi = (uint8_t)clampi(nearest_int((x[64 * p + 32 + lv] + dm1) / d1), 0, 15);
+            blk[16 + 32 * p + lv] = (uint8_t)(lo | (hi << 4));
+        }
+    }
+}
+
+// utils.rs:65-202 make_qx_quants(16, nmax, x, ls, rmse_type = 1)
+__device__ float make_qx_quants16(int nmax, const float* x, int8_t* ls) {
+    const int n = 16;
+    float max = 0.0f, amax = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
+        }
+    }
+    if (amax == 0.0f) {
+        for (int i = 0; i < n; i++) ls[i] = 0;
+        return 0.0f;
+    }
+    const float iscale = -(float)nmax / max;
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float xi = x[i];
+        const int32_t l = clampi(nearest_int(iscale * xi), -nmax, nmax - 1);
+        ls[i] = (int8_t)(l + nmax);
+        const float w = xi * xi;
+        const float lf = (float)l;
+        sumlx += w * xi * lf;
+        suml2 += w * lf * lf;
+    }
+    float scale = sumlx / suml2;
+    float best = scale * sumlx;
+    for (int itry = 0; itry < 3; itry++) {
+        const float is2 = 1.0f / scale;
+        float slx = 0.0f, sl2 = 0.0f;
+        bool changed = false;
+        for (int i = 0; i < n; i++) {
+            const float xi = x[i];
+            const int32_t l = clampi(nearest_int(is2 * xi), -nmax, nmax - 1);
+            if (l + nmax != (int32_t)ls[i]) changed = true;
+            const float w = xi * xi;
+            const float lf = (float)l;
+            slx += w * xi * lf;
+            sl2 += w * lf * lf;
+        }
+        if (!changed || sl2 == 0.0f || slx * slx <= best * sl2) break;
+        for (int i = 0; i < n; i++) {
+            const int32_t l = nearest_int(is2 * x[i]);
+            ls[i] = (int8_t)(nmax + clampi(l, -nmax, nmax - 1));
+        }
+        sumlx = slx;
+        suml2 = sl2;
+        scale = sumlx / suml2;
+        best = scale * sumlx;
+    }
+    for (int itry = 0; itry < 5; itry++) {
+        int n_changed = 0;
+        for (int i = 0; i < n; i++) {
+            const float xi = x[i];
+            const float w = xi * xi;
+            const int32_t l = (int32_t)ls[i] - nmax;
+            float slx = sumlx - w * xi * (float)l;
+            if (slx > 0.0f) {
+                float sl2 = suml2 - w * (float)l * (float)l;
+                const int32_t new_l = clampi(nearest_int(xi * sl2 / slx), -nmax, nmax - 1);
+                if (new_l != l) {
+                    slx += w * xi * (float)new_l;
+                    sl2 += w * (float)new_l * (float)new_l;
+                    if (sl2 > 0.0f && slx * slx * suml2 > sumlx * sumlx * sl2) {
+                        ls[i] = (int8_t)(nmax + new_l);
+                        sumlx = slx;
+                        suml2 = sl2;
+                        scale = sumlx / suml2;
+                        best = scale * sumlx;
+                        n_changed++;
+                    }
+                }
+            }
+        }
+        if (n_changed == 0) break;
+    }
+    (void)best;
+    return scale;
+}
+
+// k_quants.rs:1801-1871
+__global__ void w_q6k_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t bi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (bi >= nblocks) return;
+    const float* x = xin + bi * 256;
+    int8_t L[256];
+    float scales[16];
+    float max_scale = 0.0f, max_abs_scale = 0.0f;
+    for (int ib = 0; ib < 16; ib++) {
+        const float scale = make_qx_quants16(32, x + 16 * ib, L + 16 * ib);
+        scales[ib] = scale;
+        const float abs_scale = fabsf(scale);
+        if (abs_scale > max_abs_scale) {
+            max_abs_scale = abs_scale;
+            max_scale = scale;
+        }
+    }
+    const float iscale = -128.0f / max_scale;
+    const uint16_t dh = f32_to_f16_bits(1.0f / iscale);
+    uint8_t* y = out + bi * 210;
+    int8_t ysc[16];
+    for (int j = 0; j < 16; j++) {
+        int32_t v = nearest_int(iscale * scales[j]);
+        if (v > 127) v = 127;
+        ysc[j] = (int8_t)v;
+        y[192 + j] = (uint8_t)ysc[j];
+    }
+    y[208] = (uint8_t)dh;
+    y[209] = (uint8_t)(dh >> 8);
+    const float df = f16_bits_to_f32(dh);
+    for (int j = 0; j < 16; j++) {
+        const float d = df * (float)ysc[j];
+        if (d == 0.0f) continue;
+        for (int ii = 0; ii < 16; ii++) {
+            const int32_t ll = clampi(nearest_int(x[16 * j + ii] / d), -32, 31);
+            L[16 * j + ii] = (int8_t)(ll + 32);
+        }
+    }
+    for (int j = 0; j < 256; j += 128) {
+        uint8_t* ql = y + (j / 128) * 64;
+        uint8_t* qh = y + 128 + (j / 128) * 32;
+        for (int l = 0; l < 32; l++) {
+            const uint8_t q1 = (uint8_t)(L[j + l] & 0xF), q2 = (uint8_t)(L[j + l + 32] & 0xF);
+            const uint8_t q3 = (uint8_t)(L[j + l + 64] & 0xF), q4 = (uint8_t)(L[j + l + 96] & 0xF);
+            ql[l] = (uint8_t)(q1 | (q3 << 4));
+            ql[l + 32] = (uint8_t)(q2 | (q4 << 4));
+            qh[l] = (uint8_t)((L[j + l] >> 4) | ((L[j + l + 32] >> 4) << 2) |
+                              ((L[j + l + 64] >> 4) << 4) | ((L[j + l + 96] >> 4) << 6));
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_act(const ALayout& A, const float* x, void* ws, hipStream_t s) {
+    uint8_t* b = static_cast<uint8_t*>(ws);
+    if (A.m == 0) return hipSuccess;
+    if (A.act_dtype == XNQ_Q8K) {
+        const size_t nblocks = A.m * (A.k / 256);
+        const unsigned grid = (unsigned)((nblocks + 3) / 4);
+        quantize_q8k_kernel<false><<<grid, 256, 0, s>>>(
+            x, nblocks, A.k / 256, reinterpret_cast<int8_t*>(b + A.off_q),
+            reinterpret_cast<float*>(b + A.off_d), reinterpret_cast<int16_t*>(b + A.off_s), nullptr);
+    } else {
+        const size_t nblocks = A.m * (A.k / 32);
+        const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+        quantize_q80_kernel<false><<<grid, 256, 0, s>>>(
+            x, nblocks, reinterpret_cast<int8_t*>(b + A.off_q),
+            reinterpret_cast<uint16_t*>(b + A.off_d), reinterpret_cast<int16_t*>(b + A.off_s),
+            nullptr);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const float* x,
+                                      void* blocks, hipStream_t s) {
+    uint8_t* b = static_cast<uint8_t*>(blocks);
+    if (m == 0) return hipSuccess;
+    if (act_dtype == XNQ_Q8K) {
+        const size_t nblocks = m * (k / 256);
+        const unsigned grid = (unsigned)((nblocks + 3) / 4);
+        quantize_q8k_kernel<true><<<grid, 256, 0, s>>>(x, nblocks, k / 256, nullptr, nullptr,
+                                                        nullptr, b);
+    } else {
+        const size_t nblocks = m * (k / 32);
+        const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+        quantize_q80_kernel<true><<<grid, 256, 0, s>>>(x, nblocks, nullptr, nullptr, nullptr, b);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float* x, void* gguf,
+                                    hipStream_t s) {
+    if (nblocks == 0) return hipSuccess;
+    uint8_t* out = static_cast<uint8_t*>(gguf);
+    const unsigned threads = 64;
+    const unsigned grid = (unsigned)((nblocks + threads - 1) / threads);
+    switch (dtype) {
+    case XNQ_Q8_0: w_q80_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q4_0: w_q40_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q4K: w_q4k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q6K: w_q6k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace xnq

@@ -1,0 +1,458 @@
+// The C ABI of libxnq (include/xnq.h): device qtensors, validation and the
+// batch-size routing of matmul_t.  Kernels live in k_*.hip.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "xnq_internal.h"
+
+struct xnq_qtensor {
+    int device;
+    xnq::WLayout L;
+    void* buf;
+};
+
+namespace xnq {
+
+namespace {
+
+thread_local std::string g_err;
+std::atomic<int> g_route{0};
+
+xnq_status fail(xnq_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return st;
+}
+
+xnq_status hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? XNQ_ERR_OOM : XNQ_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+// Makes `dev` current for the scope and restores the caller's device.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) err = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+const char* dtype_name(uint32_t dt) {
+    switch (dt) {
+    case 0: return "F32";
+    case 1: return "F16";
+    case 2: return "Q4_0";
+    case 3: return "Q4_1";
+    case 6: return "Q5_0";
+    case 7: return "Q5_1";
+    case 8: return "Q8_0";
+    case 9: return "Q8_1";
+    case 10: return "Q2K";
+    case 11: return "Q3K";
+    case 12: return "Q4K";
+    case 13: return "Q5K";
+    case 14: return "Q6K";
+    case 15: return "Q8K";
+    case 30: return "BF16";
+    }
+    return nullptr;
+}
+
+bool device_dtype(uint32_t dt) {
+    return dt == XNQ_Q4_0 || dt == XNQ_Q8_0 || dt == XNQ_Q4K || dt == XNQ_Q6K;
+}
+
+// Validation shared by the weight constructors (mod.rs:262-274 check_shape,
+// mod.rs:114 unknown dtype, lib.rs:284-287 unsupported on the device).
+xnq_status check_weight(uint32_t dtype, size_t n, size_t k) {
+    const char* name = dtype_name(dtype);
+    if (!name) return fail(XNQ_ERR_INVALID, "unknown dtype for tensor %u", dtype);
+    if (!device_dtype(dtype))
+        return fail(XNQ_ERR_UNSUPPORTED, "%s quantization is not supported on the HIP device", name);
+    const size_t bs = block_size(dtype);
+    if (k == 0 || k % bs != 0)
+        return fail(XNQ_ERR_INVALID,
+                    "quantized tensor must have their last dim divisible by block size [%zu, %zu] %zu",
+                    n, k, bs);
+    if (n > 0xffffffffull || k > 0x7fffffffull)
+        return fail(XNQ_ERR_INVALID, "tensor too large [%zu, %zu]", n, k);
+    return XNQ_OK;
+}
+
+xnq_status alloc_qtensor(int device, uint32_t dtype, size_t n, size_t k, xnq_qtensor** out) {
+    WLayout L;
+    std::string err;
+    if (!weight_layout(dtype, n, k, &L, &err)) return fail(XNQ_ERR_INVALID, "%s", err.c_str());
+    void* buf = nullptr;
+    hipError_t e = hipMalloc(&buf, L.bytes ? L.bytes : kAlign);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(qtensor)");
+    xnq_qtensor* qt = new xnq_qtensor;
+    qt->device = device;
+    qt->L = L;
+    qt->buf = buf;
+    *out = qt;
+    return XNQ_OK;
+}
+
+}  // namespace
+
+size_t type_size(uint32_t dt) {
+    switch (dt) {
+    case XNQ_F32: return 4;
+    case XNQ_F16: return 2;
+    case XNQ_Q4_0: return 18;
+    case XNQ_Q8_0: return 34;
+    case XNQ_Q4K: return 144;
+    case XNQ_Q6K: return 210;
+    case XNQ_Q8K: return 292;
+    }
+    return 0;
+}
+
+size_t block_size(uint32_t dt) {
+    switch (dt) {
+    case XNQ_F32:
+    case XNQ_F16: return 1;
+    case XNQ_Q4_0:
+    case XNQ_Q8_0: return 32;
+    case XNQ_Q4K:
+    case XNQ_Q6K:
+    case XNQ_Q8K: return 256;
+    }
+    return 0;
+}
+
+uint32_t vec_dot_type(uint32_t wdt) {
+    return (wdt == XNQ_Q4_0 || wdt == XNQ_Q8_0) ? (uint32_t)XNQ_Q8_0 : (uint32_t)XNQ_Q8K;
+}
+
+bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string* err) {
+    WLayout L;
+    L.dtype = dtype;
+    L.n = n;
+    L.k = k;
+    const size_t bs = block_size(dtype);
+    if (!bs || k % bs) {
+        *err = "bad weight shape";
+        return false;
+    }
+    L.nb = k / bs;
+    switch (dtype) {
+    case XNQ_Q8_0: L.q_row = L.nb * 32; L.d_row = L.nb * 2; break;
+    case XNQ_Q4_0: L.q_row = L.nb * 16; L.d_row = L.nb * 2; break;
+    case XNQ_Q4K: L.q_row = L.nb * 128; L.s_row = L.nb * 16; break;
+    case XNQ_Q6K: L.q_row = L.nb * 128; L.h_row = L.nb * 64; L.s_row = L.nb * 16; L.d_row = L.nb * 2; break;
+    default: *err = "unsupported dtype"; return false;
+    }
+    size_t off = 0;
+    L.off_q = off;
+    off = align_up(off + L.q_row * n);
+    L.off_h = off;
+    off = align_up(off + L.h_row * n);
+    L.off_s = off;
+    off = align_up(off + L.s_row * n);
+    L.off_d = off;
+    off = align_up(off + L.d_row * n);
+    L.bytes = off;
+    *out = L;
+    return true;
+}
+
+ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k) {
+    ALayout A;
+    A.act_dtype = vec_dot_type(weight_dtype);
+    A.m = m;
+    A.k = k;
+    size_t off = 0;
+    A.off_q = off;
+    off = align_up(off + m * k);
+    if (A.act_dtype == XNQ_Q8K) {
+        A.d_per_row = k / 256;
+        A.s_per_row = k / 16;
+        A.off_d = off;
+        off = align_up(off + m * A.d_per_row * 4);
+    } else {
+        A.d_per_row = k / 32;
+        A.s_per_row = k / 32;
+        A.off_d = off;
+        off = align_up(off + m * A.d_per_row * 2);
+    }
+    A.off_s = off;
+    off = align_up(off + m * A.s_per_row * 2);
+    A.bytes = off;
+    return A;
+}
+
+}  // namespace xnq
+
+using namespace xnq;
+
+extern "C" {
+
+const char* xnq_last_error(void) { return g_err.c_str(); }
+
+int xnq_abi_version(void) { return 1; }
+
+size_t xnq_type_size(uint32_t dtype) { return type_size(dtype); }
+size_t xnq_block_size(uint32_t dtype) { return block_size(dtype); }
+
+xnq_status xnq_qtensor_upload_device(int device, uint32_t dtype, const void* gguf_blocks_dev,
+                                     size_t n, size_t k, void* stream, xnq_qtensor** out) {
+    if (!out) return fail(XNQ_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    xnq_status st = check_weight(dtype, n, k);
+    if (st) return st;
+    if (!gguf_blocks_dev && n) return fail(XNQ_ERR_INVALID, "null block pointer");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    xnq_qtensor* qt = nullptr;
+    st = alloc_qtensor(device, dtype, n, k, &qt);
+    if (st) return st;
+    hipError_t e = launch_repack(qt->L, gguf_blocks_dev, qt->buf, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        (void)hipFree(qt->buf);
+        delete qt;
+        return hip_fail(e, "repack");
+    }
+    *out = qt;
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_upload(int device, uint32_t dtype, const void* gguf_blocks_host, size_t n,
+                              size_t k, void* stream, xnq_qtensor** out) {
+    if (!out) return fail(XNQ_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    xnq_status st = check_weight(dtype, n, k);
+    if (st) return st;
+    if (!gguf_blocks_host && n) return fail(XNQ_ERR_INVALID, "null block pointer");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t bytes = n * (k / block_size(dtype)) * type_size(dtype);
+    void* tmp = nullptr;
+    hipError_t e = hipMallocAsync(&tmp, bytes ? bytes : kAlign, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(upload)");
+    e = hipMemcpyAsync(tmp, gguf_blocks_host, bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) {
+        (void)hipFreeAsync(tmp, s);
+        return hip_fail(e, "hipMemcpyAsync(upload)");
+    }
+    st = xnq_qtensor_upload_device(device, dtype, tmp, n, k, stream, out);
+    (void)hipFreeAsync(tmp, s);
+    e = hipStreamSynchronize(s);
+    if (st) return st;
+    if (e != hipSuccess) {
+        xnq_qtensor_free(*out);
+        *out = nullptr;
+        return hip_fail(e, "hipStreamSynchronize(upload)");
+    }
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_quantize(int device, uint32_t dtype, const float* src_dev, size_t n,
+                                size_t k, void* stream, xnq_qtensor** out) {
+    if (!out) return fail(XNQ_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    xnq_status st = check_weight(dtype, n, k);
+    if (st) return st;
+    if (!src_dev && n) return fail(XNQ_ERR_INVALID, "null source pointer");
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t nblocks = n * (k / block_size(dtype));
+    void* tmp = nullptr;
+    hipError_t e = hipMallocAsync(&tmp, nblocks ? nblocks * type_size(dtype) : kAlign, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(quantize)");
+    e = launch_weight_from_float(dtype, nblocks, src_dev, tmp, s);
+    if (e != hipSuccess) {
+        (void)hipFreeAsync(tmp, s);
+        return hip_fail(e, "quantize kernel");
+    }
+    st = xnq_qtensor_upload_device(device, dtype, tmp, n, k, stream, out);
+    (void)hipFreeAsync(tmp, s);
+    return st;
+}
+
+void xnq_qtensor_free(xnq_qtensor* qt) {
+    if (!qt) return;
+    DeviceGuard g(qt->device);
+    (void)hipFree(qt->buf);
+    delete qt;
+}
+
+uint32_t xnq_qtensor_dtype(const xnq_qtensor* qt) { return qt ? qt->L.dtype : 0; }
+size_t xnq_qtensor_rows(const xnq_qtensor* qt) { return qt ? qt->L.n : 0; }
+size_t xnq_qtensor_cols(const xnq_qtensor* qt) { return qt ? qt->L.k : 0; }
+int xnq_qtensor_device(const xnq_qtensor* qt) { return qt ? qt->device : -1; }
+size_t xnq_qtensor_storage_size(const xnq_qtensor* qt) {
+    return qt ? qt->L.n * qt->L.nb * type_size(qt->L.dtype) : 0;
+}
+size_t xnq_qtensor_device_bytes(const xnq_qtensor* qt) { return qt ? qt->L.bytes : 0; }
+
+size_t xnq_lhs_workspace_size(uint32_t weight_dtype, size_t m, size_t k) {
+    if (!device_dtype(weight_dtype)) return 0;
+    return act_layout(weight_dtype, m, k).bytes;
+}
+
+static xnq_status check_lhs(uint32_t weight_dtype, size_t k) {
+    const uint32_t vt = vec_dot_type(weight_dtype);
+    const size_t bs = block_size(vt);
+    if (k % bs != 0)
+        return fail(XNQ_ERR_INVALID, "quantize_row_%s: %zu is not divisible by %zu",
+                    vt == XNQ_Q8K ? "q8k" : "q8_0", k, bs);
+    return XNQ_OK;
+}
+
+xnq_status xnq_quantize_lhs(uint32_t weight_dtype, size_t m, size_t k, const float* lhs_dev,
+                            void* workspace_dev, void* stream) {
+    if (!device_dtype(weight_dtype))
+        return fail(XNQ_ERR_UNSUPPORTED, "no device activation quantizer for dtype %u", weight_dtype);
+    xnq_status st = check_lhs(weight_dtype, k);
+    if (st) return st;
+    if (m == 0) return XNQ_OK;
+    if (!lhs_dev || !workspace_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    const ALayout A = act_layout(weight_dtype, m, k);
+    hipError_t e = launch_quantize_act(A, lhs_dev, workspace_dev, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize_lhs");
+    return XNQ_OK;
+}
+
+xnq_status xnq_set_route(int route) {
+    if (route < 0 || route > 2) return fail(XNQ_ERR_INVALID, "route must be 0, 1 or 2");
+    g_route.store(route);
+    return XNQ_OK;
+}
+
+static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n) {
+    if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");
+    if (k != qt->L.k || n != qt->L.n)
+        return fail(XNQ_ERR_INVALID, "matmul_t: mkn (%zu, %zu, %zu) does not match weight [%zu, %zu]",
+                    m, k, n, qt->L.n, qt->L.k);
+    if (m > 0x7fffffffull) return fail(XNQ_ERR_INVALID, "m too large: %zu", m);
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                   const void* workspace_dev, float* dst_dev, void* stream) {
+    xnq_status st = check_mkn(qt, m, k, n);
+    if (st) return st;
+    if (m == 0 || n == 0) return XNQ_OK;
+    if (!workspace_dev || !dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    DeviceGuard g(qt->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    const WView w = make_wview(qt->L, qt->buf);
+    const AView a = make_aview(act_layout(qt->L.dtype, m, k), workspace_dev);
+    const int route = g_route.load();
+    hipError_t e;
+    const bool use_mfma = route == 2 || (route == 0 && m > 8 && mfma_supported(qt->L.dtype, m, n, k));
+    if (use_mfma) {
+        if (!mfma_supported(qt->L.dtype, m, n, k))
+            return fail(XNQ_ERR_UNSUPPORTED, "no MFMA kernel for this dtype/shape");
+        e = launch_mfma(w, a, m, dst_dev, (hipStream_t)stream);
+    } else {
+        e = launch_matvec(w, a, m, dst_dev, (hipStream_t)stream);
+    }
+    if (e == hipErrorInvalidConfiguration)
+        return fail(XNQ_ERR_INVALID, "k = %zu is too large for the matvec kernel's LDS", k);
+    if (e != hipSuccess) return hip_fail(e, "matmul kernel");
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                const float* lhs_dev, float* dst_dev, void* stream) {
+    xnq_status st = check_mkn(qt, m, k, n);
+    if (st) return st;
+    st = check_lhs(qt->L.dtype, k);
+    if (st) return st;
+    if (m == 0 || n == 0) return XNQ_OK;
+    if (!lhs_dev || !dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    DeviceGuard g(qt->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t s = (hipStream_t)stream;
+    const ALayout A = act_layout(qt->L.dtype, m, k);
+    void* ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, A.bytes, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(workspace)");
+    st = xnq_quantize_lhs(qt->L.dtype, m, k, lhs_dev, ws, stream);
+    if (!st) st = xnq_qtensor_matmul_preq(qt, m, k, n, ws, dst_dev, stream);
+    (void)hipFreeAsync(ws, s);
+    return st;
+}
+
+xnq_status xnq_qtensor_dequantize(const xnq_qtensor* qt, float* dst_dev, size_t elem_count,
+                                  void* stream) {
+    if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");
+    if (elem_count != qt->L.n * qt->L.k)
+        return fail(XNQ_ERR_INVALID, "dequantize: ys (len = %zu) does not match the expected length of %zu",
+                    elem_count, qt->L.n * qt->L.k);
+    if (elem_count == 0) return XNQ_OK;
+    if (!dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    DeviceGuard g(qt->device);
+    hipError_t e = launch_dequant(qt->L, qt->buf, dst_dev, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dequantize");
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_raw_data(const xnq_qtensor* qt, void* host_dst, size_t cap, void* stream) {
+    if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");
+    const size_t bytes = xnq_qtensor_storage_size(qt);
+    if (cap < bytes) return fail(XNQ_ERR_INVALID, "raw_data: buffer too small (%zu < %zu)", cap, bytes);
+    if (bytes == 0) return XNQ_OK;
+    if (!host_dst) return fail(XNQ_ERR_INVALID, "null pointer");
+    DeviceGuard g(qt->device);
+    hipStream_t s = (hipStream_t)stream;
+    void* tmp = nullptr;
+    hipError_t e = hipMallocAsync(&tmp, bytes, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(raw_data)");
+    e = launch_unrepack(qt->L, qt->buf, tmp, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(host_dst, tmp, bytes, hipMemcpyDeviceToHost, s);
+    (void)hipFreeAsync(tmp, s);
+    hipError_t e2 = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "raw_data");
+    if (e2 != hipSuccess) return hip_fail(e2, "hipStreamSynchronize(raw_data)");
+    return XNQ_OK;
+}
+
+xnq_status xnq_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const float* src_dev,
+                                   void* blocks_dev, void* stream) {
+    if (act_dtype != XNQ_Q8_0 && act_dtype != XNQ_Q8K)
+        return fail(XNQ_ERR_UNSUPPORTED, "activation dtype must be Q8_0 or Q8K, got %u", act_dtype);
+    const size_t bs = block_size(act_dtype);
+    if (k % bs != 0)
+        return fail(XNQ_ERR_INVALID, "%zu is not divisible by %zu", k, bs);
+    if (m == 0) return XNQ_OK;
+    if (!src_dev || !blocks_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    hipError_t e = launch_quantize_act_blocks(act_dtype, m, k, src_dev, blocks_dev, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize_act_blocks");
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* workspace_dev,
+                                  int32_t* out_dev, void* stream) {
+    if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");
+    if (m == 0) return XNQ_OK;
+    if (!workspace_dev || !out_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    DeviceGuard g(qt->device);
+    const WView w = make_wview(qt->L, qt->buf);
+    const AView a = make_aview(act_layout(qt->L.dtype, m, qt->L.k), workspace_dev);
+    hipError_t e = launch_block_ints(w, a, m, out_dev, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "block_ints");
+    return XNQ_OK;
+}
+
+}  // extern "C"

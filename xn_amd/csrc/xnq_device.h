@@ -1,0 +1,136 @@
+// Device-side helpers shared by the libxnq kernels: Rust cast semantics,
+// f16 conversion, and the per-chunk integer dot products of each GGML type.
+// A chunk is 32 consecutive elements of one weight row (see xnq_internal.h).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xnq {
+
+// ---- scalar semantics of the reference (Rust) -----------------------------
+
+// f32 `as i8`: saturating, NaN -> 0.
+__device__ __forceinline__ int8_t f_as_i8(float v) {
+    if (v != v) return 0;
+    if (v <= -128.0f) return -128;
+    if (v >= 127.0f) return 127;
+    return (int8_t)(int)v;
+}
+__device__ __forceinline__ uint8_t f_as_u8(float v) {
+    if (v != v) return 0;
+    if (v <= 0.0f) return 0;
+    if (v >= 255.0f) return 255;
+    return (uint8_t)(int)v;
+}
+__device__ __forceinline__ int32_t f_as_i32(float v) {
+    if (v != v) return 0;
+    if (v <= -2147483648.0f) return INT32_MIN;
+    if (v >= 2147483647.0f) return INT32_MAX;
+    return (int32_t)v;
+}
+// utils.rs:3-5 nearest_int: f32::round (half away from zero) then `as i32`.
+__device__ __forceinline__ int32_t nearest_int(float v) { return f_as_i32(roundf(v)); }
+__device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// IEEE binary16 conversions (round to nearest even on the way down).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+    return (float)h;
+}
+
+// ---- packed integer dots ---------------------------------------------------
+
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Sum over 32 elements of nibble * q8, with the nibble order
+//   dword w of q: low nibbles = elements 4w..4w+3, high = elements 16+4w..16+4w+3
+// and a[0..7] the 32 activation bytes as 8 dwords.
+__device__ __forceinline__ void nib_dot2(uint4 q, const int* a, int& lo, int& hi) {
+    const uint32_t M = 0x0F0F0F0Fu;
+    int l = 0, h = 0;
+    l = dot4((int)(q.x & M), a[0], l);
+    l = dot4((int)(q.y & M), a[1], l);
+    l = dot4((int)(q.z & M), a[2], l);
+    l = dot4((int)(q.w & M), a[3], l);
+    h = dot4((int)((q.x >> 4) & M), a[4], h);
+    h = dot4((int)((q.y >> 4) & M), a[5], h);
+    h = dot4((int)((q.z >> 4) & M), a[6], h);
+    h = dot4((int)((q.w >> 4) & M), a[7], h);
+    lo = l;
+    hi = h;
+}
+
+// Q4K: 6-bit scale and min of sub-block j from the 12 packed bytes
+// (utils.rs:53-63 get_scale_min_k4); s0,s1,s2 = scales bytes 0-3, 4-7, 8-11.
+__device__ __forceinline__ uint32_t byte_of3(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xffu;
+}
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                              int& sc, int& m) {
+    if (j < 4) {
+        sc = (int)(byte_of3(s0, s1, s2, j) & 63u);
+        m = (int)(byte_of3(s0, s1, s2, j + 4) & 63u);
+    } else {
+        uint32_t bj4 = byte_of3(s0, s1, s2, j + 4);
+        sc = (int)((bj4 & 0xFu) | ((byte_of3(s0, s1, s2, j - 4) >> 6) << 4));
+        m = (int)((bj4 >> 4) | ((byte_of3(s0, s1, s2, j) >> 6) << 4));
+    }
+}
+
+// Q6K: the 8 dwords of 6-bit values (0..63) of one chunk.
+__device__ __forceinline__ void q6k_unpack(uint4 ql, uint2 qh, int* b) {
+    const uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x03030303u;
+    b[0] = (int)((ql.x & M4) | ((qh.x & M2) << 4));
+    b[1] = (int)((ql.y & M4) | (((qh.x >> 2) & M2) << 4));
+    b[2] = (int)((ql.z & M4) | (((qh.x >> 4) & M2) << 4));
+    b[3] = (int)((ql.w & M4) | (((qh.x >> 6) & M2) << 4));
+    b[4] = (int)(((ql.x >> 4) & M4) | ((qh.y & M2) << 4));
+    b[5] = (int)(((ql.y >> 4) & M4) | (((qh.y >> 2) & M2) << 4));
+    b[6] = (int)(((ql.z >> 4) & M4) | (((qh.y >> 4) & M2) << 4));
+    b[7] = (int)(((ql.w >> 4) & M4) | (((qh.y >> 6) & M2) << 4));
+}
+
+// Integer dot of one Q6K chunk: sc0 * sum_{16}(q6-32)*q8 + sc1 * (next 16),
+// using sum (q-32)*a = sum q*a - 32*sum a with the Q8K block sums.
+__device__ __forceinline__ int q6k_chunk_int(uint4 ql, uint2 qh, const int* a, int sc0, int sc1,
+                                             int bs0, int bs1) {
+    int b[8];
+    q6k_unpack(ql, qh, b);
+    int lo = 0, hi = 0;
+    lo = dot4(b[0], a[0], lo);
+    lo = dot4(b[1], a[1], lo);
+    lo = dot4(b[2], a[2], lo);
+    lo = dot4(b[3], a[3], lo);
+    hi = dot4(b[4], a[4], hi);
+    hi = dot4(b[5], a[5], hi);
+    hi = dot4(b[6], a[6], hi);
+    hi = dot4(b[7], a[7], hi);
+    return sc0 * (lo - 32 * bs0) + sc1 * (hi - 32 * bs1);
+}
+
+// Sum of 32 signed bytes x signed bytes.
+__device__ __forceinline__ int i8_dot32(uint4 w0, uint4 w1, const int* a) {
+    int s = 0;
+    s = dot4((int)w0.x, a[0], s);
+    s = dot4((int)w0.y, a[1], s);
+    s = dot4((int)w0.z, a[2], s);
+    s = dot4((int)w0.w, a[3], s);
+    s = dot4((int)w1.x, a[4], s);
+    s = dot4((int)w1.y, a[5], s);
+    s = dot4((int)w1.z, a[6], s);
+    s = dot4((int)w1.w, a[7], s);
+    return s;
+}
+
+}  // namespace xnq

@@ -1,0 +1,138 @@
+// Internal declarations shared by the libxnq translation units: the repacked
+// weight layout in HBM, the private activation workspace layout, small device
+// helpers and the launchers each .hip file provides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/xnq.h"
+
+namespace xnq {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr size_t kAlign = 256;
+
+inline size_t align_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------------------
+// Repacked weight storage.  Every plane is row major over the n weight rows,
+// so one row of one plane is a contiguous run of bytes; a wavefront working
+// on a row reads 1 KiB per dwordx4 instruction.
+//
+// A "chunk" is 32 consecutive elements of a row: the unit one lane handles.
+//   Q8_0: q plane [n][nb][32] int8      d plane [n][nb] f16
+//   Q4_0: q plane [n][nb][16] nibbles   d plane [n][nb] f16
+//         byte i: low nibble = element i, high nibble = element i+16
+//         (the GGUF order, already what the dot4 grouping wants)
+//   Q4K:  q plane [n][nb][8 chunks][16] s plane [n][nb][16] = {d, dmin, scales[12]}
+//         chunk c = sub-block c; byte i: low = element i, high = element i+16
+//   Q6K:  q plane [n][nb][8][16] low 4 bits, nibble order as Q4K
+//         h plane [n][nb][8][8]  high 2 bits: dword u, byte p, bits 2g'..2g'+1
+//                                hold element 4*(4u+g')+p of the chunk
+//         s plane [n][nb][16] int8 scales, d plane [n][nb] f16
+// nb = blocks per row (k/32 for Q4_0/Q8_0, k/256 for Q4K/Q6K).
+// ---------------------------------------------------------------------------
+struct WLayout {
+    uint32_t dtype = 0;
+    size_t n = 0, k = 0, nb = 0;
+    size_t q_row = 0, h_row = 0, s_row = 0, d_row = 0;  // bytes per row, per plane
+    size_t off_q = 0, off_h = 0, off_s = 0, off_d = 0;  // plane offsets in the allocation
+    size_t bytes = 0;
+};
+
+// Plain-pointer view passed to kernels by value.
+struct WView {
+    const uint8_t* q;
+    const uint8_t* h;
+    const uint8_t* s;
+    const uint8_t* d;
+    uint32_t q_row, h_row, s_row, d_row;
+    uint32_t n, k, nb;
+    uint32_t dtype;
+};
+
+// ---------------------------------------------------------------------------
+// Quantized activation workspace (private layout):
+//   Q8K  (for Q4K/Q6K weights): q [m][k] int8, d [m][k/256] f32, sums [m][k/16] int16 (bsums)
+//   Q8_0 (for Q4_0/Q8_0):       q [m][k] int8, d [m][k/32] f16,  sums [m][k/32] int16
+// ---------------------------------------------------------------------------
+struct ALayout {
+    uint32_t act_dtype = 0;
+    size_t m = 0, k = 0;
+    size_t off_q = 0, off_d = 0, off_s = 0, bytes = 0;
+    size_t d_per_row = 0, s_per_row = 0;  // entries per row
+};
+
+struct AView {
+    const int8_t* q;
+    const uint8_t* d;  // f32 (Q8K) or f16 (Q8_0)
+    const int16_t* s;
+    uint32_t m, k;
+    uint32_t d_per_row, s_per_row;
+};
+
+bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string* err);
+ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k);
+uint32_t vec_dot_type(uint32_t weight_dtype);
+size_t type_size(uint32_t dtype);
+size_t block_size(uint32_t dtype);
+
+inline WView make_wview(const WLayout& L, const void* base) {
+    const uint8_t* b = static_cast<const uint8_t*>(base);
+    WView v;
+    v.q = b + L.off_q;
+    v.h = b + L.off_h;
+    v.s = b + L.off_s;
+    v.d = b + L.off_d;
+    v.q_row = (uint32_t)L.q_row;
+    v.h_row = (uint32_t)L.h_row;
+    v.s_row = (uint32_t)L.s_row;
+    v.d_row = (uint32_t)L.d_row;
+    v.n = (uint32_t)L.n;
+    v.k = (uint32_t)L.k;
+    v.nb = (uint32_t)L.nb;
+    v.dtype = L.dtype;
+    return v;
+}
+
+inline AView make_aview(const ALayout& A, const void* base) {
+    const uint8_t* b = static_cast<const uint8_t*>(base);
+    AView v;
+    v.q = reinterpret_cast<const int8_t*>(b + A.off_q);
+    v.d = b + A.off_d;
+    v.s = reinterpret_cast<const int16_t*>(b + A.off_s);
+    v.m = (uint32_t)A.m;
+    v.k = (uint32_t)A.k;
+    v.d_per_row = (uint32_t)A.d_per_row;
+    v.s_per_row = (uint32_t)A.s_per_row;
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (each returns hipSuccess or the first HIP error).
+// ---------------------------------------------------------------------------
+// k_repack.hip
+hipError_t launch_repack(const WLayout& L, const void* gguf_dev, void* dst_dev, hipStream_t s);
+hipError_t launch_unrepack(const WLayout& L, const void* src_dev, void* gguf_dev, hipStream_t s);
+hipError_t launch_dequant(const WLayout& L, const void* src_dev, float* y, hipStream_t s);
+// k_quantize.hip
+hipError_t launch_quantize_act(const ALayout& A, const float* x, void* ws, hipStream_t s);
+hipError_t launch_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const float* x,
+                                      void* blocks, hipStream_t s);
+hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float* x, void* gguf,
+                                    hipStream_t s);
+// k_matvec.hip
+hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hipStream_t s);
+hipError_t launch_block_ints(const WView& w, const AView& a, size_t m,
+                             int32_t* out, hipStream_t s);
+// k_mfma.hip
+bool mfma_supported(uint32_t dtype, size_t m, size_t n, size_t k);
+hipError_t launch_mfma(const WView& w, const AView& a, size_t m, float* y,
+                       hipStream_t s);
+
+}  // namespace xnq
