@@ -66,9 +66,10 @@ def time_graph(g, stream, reps: int = 5) -> float:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        start.record(stream)
-        g.replay()
-        end.record(stream)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            g.replay()
+            end.record(stream)
         end.synchronize()
         times.append(start.elapsed_time(end))
     return float(np.median(times))
@@ -206,7 +207,7 @@ def main():
 
         threads = min(os.cpu_count() or 1, 16)
         oracle.cpu_pool_init(threads)
-        ncopies = 4
+        ncopies = min(16, len(copies))  # > 512 MB, past any host L3
         host_w = [np.frombuffer(copies[i].data(), dtype=np.uint8) for i in range(ncopies)]
         xh = np.random.default_rng(1).normal(0, 1, (1, K_DIM)).astype(np.float32)
         scratch = np.zeros(oracle.nbytes(oracle.Q8K, K_DIM), dtype=np.uint8)

@@ -37,7 +37,11 @@ __device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
 }
 
 // IEEE binary16 conversions (round to nearest even on the way down).
+// The empty asm keeps the compiler from fusing the conversion with the
+// multiply that produced `f` (a mixed-precision fma with a +0 addend, which
+// would turn a -0 product into +0).
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    __asm__ volatile("" : "+v"(f));
     _Float16 h = (_Float16)f;
     return __builtin_bit_cast(uint16_t, h);
 }
