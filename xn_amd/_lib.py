@@ -9,7 +9,7 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libxnq.so")
+LIB_PATH = os.environ.get("XNQ_LIB_PATH") or os.path.join(_HERE, "libxnq.so")
 
 _lock = threading.Lock()
 _lib = None

@@ -1,0 +1,432 @@
+// Decode-path matmul for m <= 8 activation rows (template; instantiated per
+// weight dtype in k_matvec_<dtype>.hip).
+//
+// Work split: a wavefront owns R consecutive weight rows ("row group") and,
+// for each row, CPL 32-element chunks per lane (chunk c = lane + 64*v), i.e.
+// every dwordx4 load instruction of the wavefront covers 1 KiB of one plane.
+// All R*CPL loads of a row group are issued before anything else happens, so
+// the whole weight stream is in flight while the activations are staged; the
+// grid is sized so every row group of the common shapes is resident at once.
+//
+// Activations live in LDS: either quantized there by the workgroup itself
+// from the f32 rows (FUSED, m == 1: one kernel per matmul call, no
+// workspace) or copied from a Q8 workspace produced by the quantize kernel.
+// Integer dot products use v_dot4_i32_i8; block scales are applied in f32.
+#pragma once
+
+#include <cstdlib>
+#include <map>
+#include <mutex>
+
+#include "xnq_device.h"
+#include "xnq_internal.h"
+#include "xnq_quant_dev.h"
+
+namespace xnq {
+namespace mv {
+
+constexpr int kWave = 64;
+constexpr uint32_t kMaxLds = 160 * 1024;
+
+// LDS holds MB consecutive activation row images (ActImg in xnq_internal.h),
+// the same bytes as the quantized workspace, so staging is a flat copy.
+__host__ __device__ inline uint32_t lds_bytes(int mb, uint32_t k, bool kquant) {
+    return (uint32_t)mb * act_img(k, kquant).row_bytes;
+}
+
+// Sum over the 64 lanes with DPP: row_shr 1/2/4/8 build each 16-lane row's
+// total in its last lane, row_bcast 15/31 carry it across rows; lane 63 ends
+// up with the wavefront total, which readlane broadcasts.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int t = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true);
+    return v + __int_as_float(t);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = dpp_add<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_add<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_add<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15
+    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Copy MB row images of the quantized workspace into LDS; rows past mcount
+// are zero.  Loads are issued in batches of kBatch before any LDS write so one
+// memory round trip covers the whole batch.
+template <int MB, int NW>
+__device__ void stage_activations(const AView& a, uint32_t m0, uint32_t mcount, uint8_t* lds) {
+    constexpr int kBatch = 8;
+    constexpr int kThreads = NW * kWave;
+    const uint32_t rb = a.A.row_bytes;
+    const uint32_t total = (uint32_t)MB * rb / 16, live = (mcount < (uint32_t)MB ? mcount : MB) * rb / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(a.img + (size_t)m0 * rb);
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    for (uint32_t base = 0; base < total; base += kBatch * kThreads) {
+        uint4 v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++) {
+            const uint32_t i = base + j * kThreads + threadIdx.x;
+            v[j] = i < live ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; j++) {
+            const uint32_t i = base + j * kThreads + threadIdx.x;
+            if (i < total) dst[i] = v[j];
+        }
+    }
+}
+
+// Quantize MB f32 rows straight into the LDS images (the same bytes as the
+// standalone quantize kernel: both go through q8k/q80 quant + store).
+template <int DT, int MB, int kNW>
+__device__ void quantize_into_lds(const float* __restrict__ x, uint32_t k, uint32_t m0,
+                                  uint32_t mcount, uint8_t* lds) {
+    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    constexpr int kBatch = 2;
+    const ActImg A = act_img(k, kq);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    if (kq) {
+        const uint32_t nb = k / 256, total = MB * nb;
+        for (uint32_t b0 = wave; b0 < total; b0 += kBatch * kNW) {  // uniform per wavefront
+            float4 v[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const uint32_t b = b0 + j * kNW, mb = b / nb, bb = b % nb;
+                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (b < total && mb < mcount)
+                    v[j] = reinterpret_cast<const float4*>(x + (size_t)(m0 + mb) * k + bb * 256)[lane];
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const uint32_t b = b0 + j * kNW;
+                if (b < total) {
+                    const Q8KLane r = q8k_quant_wave(v[j], lane);
+                    q8k_store(lds + (b / nb) * A.row_bytes, A, b % nb, lane, r);
+                }
+            }
+        }
+    } else {
+        const uint32_t nb = k / 32, total = MB * nb;
+        const int sub = lane & 7;
+        for (uint32_t b0 = wave * 8; b0 < total; b0 += kBatch * kNW * 8) {  // uniform per wavefront
+            float4 v[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const uint32_t b = b0 + j * kNW * 8 + (lane >> 3), mb = b / nb, c = b % nb;
+                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (b < total && mb < mcount)
+                    v[j] = reinterpret_cast<const float4*>(x + (size_t)(m0 + mb) * k + c * 32)[sub];
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const uint32_t bw = b0 + j * kNW * 8;
+                if (bw < total) {  // uniform: the whole wavefront runs the shuffles
+                    const Q80Lane r = q80_quant_8lanes(v[j]);
+                    const uint32_t b = bw + (lane >> 3);
+                    if (b < total) q80_store(lds + (b / nb) * A.row_bytes, A, b % nb, sub, r);
+                }
+            }
+        }
+    }
+}
+
+// Per-chunk weight data held in registers between the load and the compute.
+struct Chunk {
+    uint4 q;
+    uint4 x;  // Q8_0: second 16 bytes; Q4K: {d|dmin, scales}; Q6K: qh in .x/.y, scale pair in .z
+    float dw;
+};
+
+// Byte offsets are 32-bit (every plane is < 4 GiB, checked at upload), so the
+// loads use a uniform 64-bit base plus one VGPR offset.
+template <int DT>
+__device__ __forceinline__ void load_chunk(const WView& w, uint32_t row, uint32_t c, Chunk& ch) {
+    if (DT == XNQ_Q8_0) {
+        const uint32_t o = row * w.q_row + c * 32;
+        ch.q = *reinterpret_cast<const uint4*>(w.q + o);
+        ch.x = *reinterpret_cast<const uint4*>(w.q + o + 16);
+        ch.dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2)));
+    } else if (DT == XNQ_Q4_0) {
+        ch.q = *reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16));
+        ch.dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2)));
+    } else if (DT == XNQ_Q4K) {
+        ch.q = *reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16));
+        ch.x = *reinterpret_cast<const uint4*>(w.s + (row * w.s_row + (c >> 3) * 16));
+    } else {  // Q6K
+        const uint32_t sb = c >> 3, j = c & 7;
+        ch.q = *reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16));
+        const uint2 h = *reinterpret_cast<const uint2*>(w.h + (row * w.h_row + c * 8));
+        ch.x.x = h.x;
+        ch.x.y = h.y;
+        ch.x.z = *reinterpret_cast<const uint16_t*>(w.s + (row * w.s_row + sb * 16 + 2 * j));
+        ch.dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + sb * 2)));
+    }
+}
+
+template <int DT, int MB>
+__device__ __forceinline__ void compute_chunk(const Chunk& ch, uint32_t c, uint32_t k,
+                                              const uint8_t* lds, const ActImg& A, float* acc) {
+    int sc = 0, mn = 0;
+    float dw = ch.dw, dmin = 0.0f;
+    if (DT == XNQ_Q4K) {
+        dw = f16_bits_to_f32(ch.x.x);
+        dmin = f16_bits_to_f32(ch.x.x >> 16);
+        q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)(c & 7), sc, mn);
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const uint8_t* row = lds + mb * A.row_bytes;
+        const uint4 a0 = *reinterpret_cast<const uint4*>(row + c * 16);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(row + k / 2 + c * 16);
+        const int a[8] = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                          (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        const int32_t sv = reinterpret_cast<const int32_t*>(row + A.s_off)[c];
+        const float* ld = reinterpret_cast<const float*>(row + A.d_off);
+        if (DT == XNQ_Q4K) {
+            int lo, hi;
+            nib_dot2(ch.q, a, lo, hi);
+            const int isum = sc * (lo + hi);
+            const int msum = mn * ((int)(int16_t)(sv & 0xffff) + (int)(int16_t)(sv >> 16));
+            const float da = ld[c >> 3];
+            acc[mb] += (dw * da) * (float)isum - (dmin * da) * (float)msum;
+        } else if (DT == XNQ_Q6K) {
+            const int sc0 = (int)(int8_t)(ch.x.z & 0xff), sc1 = (int)(int8_t)((ch.x.z >> 8) & 0xff);
+            const int v = q6k_chunk_int(ch.q, make_uint2(ch.x.x, ch.x.y), a, sc0, sc1,
+                                        (int)(int16_t)(sv & 0xffff), (int)(int16_t)(sv >> 16));
+            const float da = ld[c >> 3];
+            acc[mb] += (dw * da) * (float)v;
+        } else if (DT == XNQ_Q4_0) {
+            int lo, hi;
+            nib_dot2(ch.q, a, lo, hi);
+            const int v = lo + hi - 8 * sv;
+            acc[mb] += (dw * ld[c]) * (float)v;
+        } else {
+            const int v = i8_dot32(ch.q, ch.x, a);
+            acc[mb] += (dw * ld[c]) * (float)v;
+        }
+    }
+}
+
+// First staging batch of the quantized workspace, loaded into registers before
+// the weight loads are issued so its (L2) latency overlaps them.
+template <int MB, int NW>
+struct StagePrefetch {
+    static constexpr int kPer = 2;
+    uint4 v[kPer];
+    __device__ __forceinline__ void load(const AView& a, uint32_t m0, uint32_t mcount) {
+        const uint32_t rb = a.A.row_bytes;
+        const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * rb / 16;
+        const uint4* src = reinterpret_cast<const uint4*>(a.img + (size_t)m0 * rb);
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const uint32_t i = j * NW * kWave + threadIdx.x;
+            v[j] = i < live ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    // Write the prefetched batch and copy whatever it did not cover.
+    __device__ __forceinline__ void store(const AView& a, uint32_t m0, uint32_t mcount, uint8_t* lds) {
+        const uint32_t rb = a.A.row_bytes;
+        const uint32_t total = (uint32_t)MB * rb / 16;
+        const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * rb / 16;
+        uint4* dst = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const uint32_t i = j * NW * kWave + threadIdx.x;
+            if (i < total) dst[i] = v[j];
+        }
+        const uint4* src = reinterpret_cast<const uint4*>(a.img + (size_t)m0 * rb);
+        for (uint32_t i = kPer * NW * kWave + threadIdx.x; i < total; i += NW * kWave)
+            dst[i] = i < live ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+};
+
+// One wavefront per row group of R rows, NW wavefronts per workgroup.
+template <int DT, int MB, int R, int CPL, int NW, bool FUSED>
+__global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const float* __restrict__ x,
+                                                         uint32_t m0, uint32_t mcount,
+                                                         float* __restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    const ActImg A = act_img(w.k, kq);
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t nchunks = w.k / 32;
+    const uint32_t npass = (nchunks + 64 * CPL - 1) / (64 * CPL);
+    const uint32_t ngroups = (w.n + R - 1) / R;
+    const uint32_t gstride = gridDim.x * NW;
+    uint32_t g = blockIdx.x * NW + wave;
+
+    Chunk ch[R][CPL];
+    auto issue = [&](uint32_t grp, uint32_t pass) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = grp * R + r;
+#pragma unroll
+            for (int v = 0; v < CPL; v++) {
+                const uint32_t c = lane + 64 * (v + CPL * pass);
+                if (row < w.n && c < nchunks) load_chunk<DT>(w, row, c, ch[r][v]);
+            }
+        }
+    };
+
+    // Activation loads first (short, L2-resident), then this wavefront's
+    // whole first row group; the activation image is built while the weight
+    // loads travel.
+    StagePrefetch<MB, NW> pre;
+    if (!FUSED) pre.load(a, m0, mcount);
+    if (g < ngroups) issue(g, 0);
+    if (FUSED) quantize_into_lds<DT, MB, NW>(x, w.k, m0, mcount, lds);
+    else pre.store(a, m0, mcount, lds);
+    __syncthreads();
+
+    for (; g < ngroups; g += gstride) {
+        float acc[R][MB];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < MB; i++) acc[r][i] = 0.0f;
+        for (uint32_t p = 0; p < npass; p++) {
+            if (p > 0) issue(g, p);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t row = g * R + r;
+#pragma unroll
+                for (int v = 0; v < CPL; v++) {
+                    const uint32_t c = lane + 64 * (v + CPL * p);
+                    if (row < w.n && c < nchunks) compute_chunk<DT, MB>(ch[r][v], c, w.k, lds, A, acc[r]);
+                }
+            }
+        }
+        const uint32_t gn = g + gstride;
+        if (gn < ngroups) issue(gn, 0);
+        float out = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < MB; i++) {
+                const float s = wave_sum(acc[r][i]);
+                if (lane == (uint32_t)(r * MB + i)) out = s;
+            }
+        const uint32_t r = lane / MB, i = lane % MB;
+        if (lane < (uint32_t)(R * MB) && i < mcount && g * R + r < w.n)
+            y[(size_t)(m0 + i) * w.n + g * R + r] = out;
+    }
+}
+
+// Occupancy (workgroups per CU) of one kernel at one LDS size, cached.
+inline int wg_per_cu(const void* fn, int threads, uint32_t lds_bytes, int* num_cu) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, uint32_t>, int> cache;
+    static int ncu = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (ncu == 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (ncu <= 0) ncu = 1;
+    }
+    *num_cu = ncu;
+    auto key = std::make_pair(fn, lds_bytes);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), threads,
+                                                     lds_bytes) != hipSuccess || occ < 1)
+        occ = 1;
+    cache[key] = occ;
+    return occ;
+}
+
+template <int DT, int MB, int R, int CPL, int NW, bool FUSED>
+hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m0, uint32_t mc,
+                      float* y, hipStream_t s) {
+    static_assert(R * MB <= 64, "one output per lane");
+    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    const uint32_t lds = lds_bytes(MB, w.k, kq);
+    auto fn = matvec_kernel<DT, MB, R, CPL, NW, FUSED>;
+    int ncu = 1;
+    const int occ = wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);
+    const uint32_t ngroups = (w.n + R - 1) / R;
+    const uint32_t need = (ngroups + NW - 1) / NW;
+    const uint32_t cap = (uint32_t)(occ * ncu);
+    const uint32_t grid = need < cap ? need : cap;
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, w, a, x, m0, mc, y);
+    return hipGetLastError();
+}
+
+inline int pick_cpl(uint32_t nchunks) {
+    return nchunks <= 64 ? 1 : nchunks <= 128 ? 2 : nchunks <= 256 ? 4 : 8;
+}
+
+inline int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+// Decode kernels read a quantized workspace (4 wavefronts per workgroup,
+// many workgroups); the fused m == 1 kernel quantizes in LDS and so uses
+// 16-wavefront workgroups to share that work.
+template <int DT, int MB, bool FUSED>
+hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const float* x, uint32_t m0,
+                      uint32_t mc, float* y, hipStream_t s) {
+    constexpr int NW = FUSED ? 16 : 4;
+#define XNQ_MV(RR, CC)                                                          \
+    if (R == RR && cpl == CC) return launch_one<DT, MB, RR, CC, NW, FUSED>(w, a, x, m0, mc, y, s);
+    if constexpr (MB == 1) {
+        XNQ_MV(1, 1) XNQ_MV(2, 1) XNQ_MV(4, 1) XNQ_MV(1, 2) XNQ_MV(2, 2) XNQ_MV(4, 2)
+        XNQ_MV(1, 4) XNQ_MV(2, 4) XNQ_MV(1, 8)
+    } else {
+        XNQ_MV(1, 1) XNQ_MV(1, 2) XNQ_MV(1, 4) XNQ_MV(1, 8)
+    }
+#undef XNQ_MV
+    return hipErrorInvalidValue;
+}
+
+// Rows per wavefront.  One row per wavefront measured fastest for every
+// shape so far (more rows per wave cost occupancy); XNQ_MV_ROWS=2|4 is a
+// tuning override.
+inline int pick_rows(uint32_t n, int cpl) {
+    (void)n;
+    static const int forced = env_int("XNQ_MV_ROWS", 0);
+    if ((forced == 2 || forced == 4) && forced * cpl <= 8) return forced;
+    return 1;
+}
+
+// y[m x n] for all m rows: FUSED quantizes from f32 `x` (m == 1 only), else
+// reads the Q8 workspace `a`.
+template <int DT>
+hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m, float* y,
+                        hipStream_t s, bool fused) {
+    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    int gmax = 8;
+    while (gmax > 1 && lds_bytes(gmax, w.k, kq) > kMaxLds) gmax >>= 1;
+    if (lds_bytes(gmax, w.k, kq) > kMaxLds) return hipErrorInvalidConfiguration;
+    const int cpl = pick_cpl(w.k / 32);
+    if (fused) {
+        if (m != 1) return hipErrorInvalidValue;
+        return launch_cpl<DT, 1, true>(pick_rows(w.n, cpl), cpl, w, a, x, 0, 1, y, s);
+    }
+    for (size_t m0 = 0; m0 < m; m0 += gmax) {
+        const uint32_t mc = (uint32_t)((m - m0) < (size_t)gmax ? (m - m0) : (size_t)gmax);
+        hipError_t e;
+        if (mc == 1) e = launch_cpl<DT, 1, false>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        else if (mc == 2) e = launch_cpl<DT, 2, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        else if (mc <= 4) e = launch_cpl<DT, 4, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        else e = launch_cpl<DT, 8, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace mv
+
+hipError_t launch_matvec_q4_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q8_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q4k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q6k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+
+}  // namespace xnq

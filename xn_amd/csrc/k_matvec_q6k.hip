@@ -1,0 +1,11 @@
+// Matvec kernels for XNQ_Q6K weights (instantiations of k_matvec_impl.h).
+#include "k_matvec_impl.h"
+
+namespace xnq {
+
+hipError_t launch_matvec_q6k(const WView& w, const AView& a, const float* x, size_t m, float* y,
+                           hipStream_t s, bool fused) {
+    return mv::launch_dtype<XNQ_Q6K>(w, a, x, m, y, s, fused);
+}
+
+}  // namespace xnq

@@ -1,0 +1,11 @@
+// Matvec kernels for XNQ_Q8_0 weights (instantiations of k_matvec_impl.h).
+#include "k_matvec_impl.h"
+
+namespace xnq {
+
+hipError_t launch_matvec_q8_0(const WView& w, const AView& a, const float* x, size_t m, float* y,
+                           hipStream_t s, bool fused) {
+    return mv::launch_dtype<XNQ_Q8_0>(w, a, x, m, y, s, fused);
+}
+
+}  // namespace xnq

@@ -8,6 +8,7 @@
 
 #include "xnq_device.h"
 #include "xnq_internal.h"
+#include "xnq_quant_dev.h"
 
 namespace xnq {
 
@@ -21,70 +22,22 @@ constexpr int kWave = 64;
 // ---------------------------------------------------------------------------
 template <bool CANONICAL>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
-                                                            size_t nblocks, size_t blocks_per_row,
-                                                            int8_t* __restrict__ q,
-                                                            float* __restrict__ dplane,
-                                                            int16_t* __restrict__ splane,
-                                                            uint8_t* __restrict__ canon) {
+                                                            size_t nblocks, ActImg A,
+                                                            uint8_t* __restrict__ out) {
     const int lane = threadIdx.x & (kWave - 1);
     const size_t blk = (size_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
-    if (blk >= nblocks) return;
+    if (blk >= nblocks) return;  // uniform over the wavefront
     const float4 v = reinterpret_cast<const float4*>(x + blk * 256)[lane];
-    const float xs[4] = {v.x, v.y, v.z, v.w};
-
-    // Largest |x|, first index on ties (the reference's strict `amax < |x|`).
-    float amax = 0.0f;
-    int idx = 0x7fffffff;
-    float max = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float a = fabsf(xs[i]);
-        if (amax < a) {
-            amax = a;
-            max = xs[i];
-            idx = lane * 4 + i;
-        }
-    }
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        float oa = __shfl_xor(amax, off);
-        int oi = __shfl_xor(idx, off);
-        float om = __shfl_xor(max, off);
-        bool take = (oa > amax) || (oa == amax && oi < idx);
-        if (take) {
-            amax = oa;
-            idx = oi;
-            max = om;
-        }
-    }
-
-    int8_t qv[4];
-    float d;
-    if (amax == 0.0f) {
-        qv[0] = qv[1] = qv[2] = qv[3] = 0;
-        d = 0.0f;
-    } else {
-        const float iscale = -128.0f / max;
-#pragma unroll
-        for (int i = 0; i < 4; i++) qv[i] = f_as_i8(fminf(roundf(iscale * xs[i]), 127.0f));
-        d = 1.0f / iscale;
-    }
-    int s = (int)qv[0] + qv[1] + qv[2] + qv[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    const uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
-                            ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
+    const Q8KLane r = q8k_quant_wave(v, lane);
     if (CANONICAL) {
         // BlockQ8K: f32 d; i8 qs[256]; i16 bsums[16]  (292 bytes, 4-byte aligned)
-        uint8_t* b = canon + blk * 292;
-        reinterpret_cast<uint32_t*>(b + 4)[lane] = packed;
-        if (lane == 0) *reinterpret_cast<float*>(b) = d;
-        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(b + 260)[lane >> 2] = (int16_t)s;
+        uint8_t* b = out + blk * 292;
+        reinterpret_cast<uint32_t*>(b + 4)[lane] = r.packed;
+        if (lane == 0) *reinterpret_cast<float*>(b) = r.d;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(b + 260)[lane >> 2] = (int16_t)r.bsum;
     } else {
-        reinterpret_cast<uint32_t*>(q + blk * 256)[lane] = packed;
-        const size_t row = blk / blocks_per_row, b = blk % blocks_per_row;
-        if (lane == 0) dplane[row * blocks_per_row + b] = d;
-        if ((lane & 3) == 0) splane[(row * blocks_per_row + b) * 16 + (lane >> 2)] = (int16_t)s;
+        const size_t bpr = A.k / 256;
+        q8k_store(out + (blk / bpr) * A.row_bytes, A, (uint32_t)(blk % bpr), lane, r);
     }
 }
 
@@ -93,47 +46,26 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 template <bool CANONICAL>
 __global__ __launch_bounds__(256) void quantize_q80_kernel(const float* __restrict__ x,
-                                                            size_t nblocks,
-                                                            int8_t* __restrict__ q,
-                                                            uint16_t* __restrict__ dplane,
-                                                            int16_t* __restrict__ splane,
-                                                            uint8_t* __restrict__ canon) {
+                                                            size_t nblocks, ActImg A,
+                                                            uint8_t* __restrict__ out) {
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t blk = t / 8;
     const int sub = (int)(t & 7);
     const bool live = blk < nblocks;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) v = reinterpret_cast<const float4*>(x + blk * 32)[sub];
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, 0.0f);
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    const int8_t q0 = f_as_i8(roundf(v.x * id)), q1 = f_as_i8(roundf(v.y * id)),
-                 q2 = f_as_i8(roundf(v.z * id)), q3 = f_as_i8(roundf(v.w * id));
-    int s = (int)q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    const Q80Lane r = q80_quant_8lanes(v);
     if (!live) return;
-    const uint16_t dh = f32_to_f16_bits(d);
     if (CANONICAL) {
         // BlockQ8_0: f16 d; i8 qs[32]  (34 bytes, 2-byte aligned)
-        uint8_t* b = canon + blk * 34;
+        uint8_t* b = out + blk * 34;
         uint16_t* w = reinterpret_cast<uint16_t*>(b + 2 + 4 * sub);
-        w[0] = (uint16_t)((uint8_t)q0 | ((uint16_t)(uint8_t)q1 << 8));
-        w[1] = (uint16_t)((uint8_t)q2 | ((uint16_t)(uint8_t)q3 << 8));
-        if (sub == 0) *reinterpret_cast<uint16_t*>(b) = dh;
+        w[0] = (uint16_t)(r.packed & 0xffffu);
+        w[1] = (uint16_t)(r.packed >> 16);
+        if (sub == 0) *reinterpret_cast<uint16_t*>(b) = r.dh;
     } else {
-        const uint32_t packed = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
-                                ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
-        reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = packed;
-        if (sub == 0) {
-            dplane[blk] = dh;
-            splane[blk] = (int16_t)s;
-        }
+        const size_t bpr = A.k / 32;
+        q80_store(out + (blk / bpr) * A.row_bytes, A, (uint32_t)(blk % bpr), sub, r);
     }
 }
 
@@ -437,22 +369,15 @@ __global__ void w_q6k_kernel(const float* __restrict__ xin, size_t nblocks, uint
 
 }  // namespace
 
-hipError_t launch_quantize_act(const ALayout& A, const float* x, void* ws, hipStream_t s) {
+hipError_t launch_quantize_act(const ALayout& L, const float* x, void* ws, hipStream_t s) {
     uint8_t* b = static_cast<uint8_t*>(ws);
-    if (A.m == 0) return hipSuccess;
-    if (A.act_dtype == XNQ_Q8K) {
-        const size_t nblocks = A.m * (A.k / 256);
-        const unsigned grid = (unsigned)((nblocks + 3) / 4);
-        quantize_q8k_kernel<false><<<grid, 256, 0, s>>>(
-            x, nblocks, A.k / 256, reinterpret_cast<int8_t*>(b + A.off_q),
-            reinterpret_cast<float*>(b + A.off_d), reinterpret_cast<int16_t*>(b + A.off_s), nullptr);
+    if (L.m == 0) return hipSuccess;
+    if (L.act_dtype == XNQ_Q8K) {
+        const size_t nblocks = L.m * (L.k / 256);
+        quantize_q8k_kernel<false><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, L.img, b);
     } else {
-        const size_t nblocks = A.m * (A.k / 32);
-        const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
-        quantize_q80_kernel<false><<<grid, 256, 0, s>>>(
-            x, nblocks, reinterpret_cast<int8_t*>(b + A.off_q),
-            reinterpret_cast<uint16_t*>(b + A.off_d), reinterpret_cast<int16_t*>(b + A.off_s),
-            nullptr);
+        const size_t nblocks = L.m * (L.k / 32);
+        quantize_q80_kernel<false><<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, nblocks, L.img, b);
     }
     return hipGetLastError();
 }
@@ -461,15 +386,13 @@ hipError_t launch_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, co
                                       void* blocks, hipStream_t s) {
     uint8_t* b = static_cast<uint8_t*>(blocks);
     if (m == 0) return hipSuccess;
+    const ActImg A = act_img((uint32_t)k, act_dtype == XNQ_Q8K);
     if (act_dtype == XNQ_Q8K) {
         const size_t nblocks = m * (k / 256);
-        const unsigned grid = (unsigned)((nblocks + 3) / 4);
-        quantize_q8k_kernel<true><<<grid, 256, 0, s>>>(x, nblocks, k / 256, nullptr, nullptr,
-                                                        nullptr, b);
+        quantize_q8k_kernel<true><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, A, b);
     } else {
         const size_t nblocks = m * (k / 32);
-        const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
-        quantize_q80_kernel<true><<<grid, 256, 0, s>>>(x, nblocks, nullptr, nullptr, nullptr, b);
+        quantize_q80_kernel<true><<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, nblocks, A, b);
     }
     return hipGetLastError();
 }

@@ -89,8 +89,9 @@ xnq_status check_weight(uint32_t dtype, size_t n, size_t k) {
         return fail(XNQ_ERR_INVALID,
                     "quantized tensor must have their last dim divisible by block size [%zu, %zu] %zu",
                     n, k, bs);
-    if (n > 0xffffffffull || k > 0x7fffffffull)
-        return fail(XNQ_ERR_INVALID, "tensor too large [%zu, %zu]", n, k);
+    // kernels address every plane with 32-bit byte offsets
+    if (n > 0xffffffffull || k > 0x7fffffffull || n * (k / bs) * type_size(dtype) >= (1ull << 32))
+        return fail(XNQ_ERR_INVALID, "tensor too large for the device layout [%zu, %zu]", n, k);
     return XNQ_OK;
 }
 
@@ -174,28 +175,13 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
 }
 
 ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k) {
-    ALayout A;
-    A.act_dtype = vec_dot_type(weight_dtype);
-    A.m = m;
-    A.k = k;
-    size_t off = 0;
-    A.off_q = off;
-    off = align_up(off + m * k);
-    if (A.act_dtype == XNQ_Q8K) {
-        A.d_per_row = k / 256;
-        A.s_per_row = k / 16;
-        A.off_d = off;
-        off = align_up(off + m * A.d_per_row * 4);
-    } else {
-        A.d_per_row = k / 32;
-        A.s_per_row = k / 32;
-        A.off_d = off;
-        off = align_up(off + m * A.d_per_row * 2);
-    }
-    A.off_s = off;
-    off = align_up(off + m * A.s_per_row * 2);
-    A.bytes = off;
-    return A;
+    ALayout L;
+    L.act_dtype = vec_dot_type(weight_dtype);
+    L.m = m;
+    L.k = k;
+    L.img = act_img((uint32_t)k, L.act_dtype == XNQ_Q8K);
+    L.bytes = align_up(m * L.img.row_bytes);
+    return L;
 }
 
 }  // namespace xnq
@@ -384,6 +370,16 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
+    const int route = g_route.load();
+    if (m == 1 && route != 2) {
+        // Decode: one kernel quantizes the row in LDS and streams the weight.
+        const WView w = make_wview(qt->L, qt->buf);
+        hipError_t e = launch_matvec_fused(w, lhs_dev, dst_dev, s);
+        if (e == hipErrorInvalidConfiguration)
+            return fail(XNQ_ERR_INVALID, "k = %zu is too large for the matvec kernel's LDS", k);
+        if (e != hipSuccess) return hip_fail(e, "matvec kernel");
+        return XNQ_OK;
+    }
     const ALayout A = act_layout(qt->L.dtype, m, k);
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, A.bytes, s);

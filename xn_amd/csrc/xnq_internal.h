@@ -57,23 +57,43 @@ struct WView {
 };
 
 // ---------------------------------------------------------------------------
-// Quantized activation workspace (private layout):
-//   Q8K  (for Q4K/Q6K weights): q [m][k] int8, d [m][k/256] f32, sums [m][k/16] int16 (bsums)
-//   Q8_0 (for Q4_0/Q8_0):       q [m][k] int8, d [m][k/32] f16,  sums [m][k/32] int16
+// Quantized activation workspace (private layout): one image per activation
+// row, row_bytes apart, byte-identical to what the matvec kernels keep in LDS.
+//   [0, K)             q8; chunk c's bytes 0-15 at c*16, bytes 16-31 at K/2 + c*16
+//                      (lane-consecutive chunks are byte-consecutive in each half)
+//   [K, K + K/8)       int32 per chunk: Q8K bsum[2c] | bsum[2c+1] << 16, Q8_0 block sum
+//   [K + K/8, ...)     f32 scale per block (K/256 blocks for Q8K, K/32 for Q8_0)
 // ---------------------------------------------------------------------------
+struct ActImg {
+    uint32_t k, s_off, d_off, row_bytes;
+};
+
+__host__ __device__ inline ActImg act_img(uint32_t k, bool kquant) {
+    ActImg A;
+    A.k = k;
+    A.s_off = k;
+    A.d_off = k + k / 8;
+    const uint32_t end = A.d_off + (kquant ? k / 64 : k / 8);
+    A.row_bytes = (end + 15u) & ~15u;
+    return A;
+}
+
+// Byte offset of activation element e (0..K-1) inside the q8 part of an image.
+__host__ __device__ inline uint32_t act_q_off(uint32_t k, uint32_t e) {
+    const uint32_t c = e >> 5, o = e & 31;
+    return (o >> 4) * (k / 2) + c * 16 + (o & 15);
+}
+
 struct ALayout {
     uint32_t act_dtype = 0;
-    size_t m = 0, k = 0;
-    size_t off_q = 0, off_d = 0, off_s = 0, bytes = 0;
-    size_t d_per_row = 0, s_per_row = 0;  // entries per row
+    size_t m = 0, k = 0, bytes = 0;
+    ActImg img{};
 };
 
 struct AView {
-    const int8_t* q;
-    const uint8_t* d;  // f32 (Q8K) or f16 (Q8_0)
-    const int16_t* s;
+    const uint8_t* img;
     uint32_t m, k;
-    uint32_t d_per_row, s_per_row;
+    ActImg A;
 };
 
 bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string* err);
@@ -100,16 +120,12 @@ inline WView make_wview(const WLayout& L, const void* base) {
     return v;
 }
 
-inline AView make_aview(const ALayout& A, const void* base) {
-    const uint8_t* b = static_cast<const uint8_t*>(base);
+inline AView make_aview(const ALayout& L, const void* base) {
     AView v;
-    v.q = reinterpret_cast<const int8_t*>(b + A.off_q);
-    v.d = b + A.off_d;
-    v.s = reinterpret_cast<const int16_t*>(b + A.off_s);
-    v.m = (uint32_t)A.m;
-    v.k = (uint32_t)A.k;
-    v.d_per_row = (uint32_t)A.d_per_row;
-    v.s_per_row = (uint32_t)A.s_per_row;
+    v.img = static_cast<const uint8_t*>(base);
+    v.m = (uint32_t)L.m;
+    v.k = (uint32_t)L.k;
+    v.A = L.img;
     return v;
 }
 
@@ -128,6 +144,8 @@ hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float*
                                     hipStream_t s);
 // k_matvec.hip
 hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hipStream_t s);
+// m == 1: quantizes the f32 row inside the kernel (no workspace).
+hipError_t launch_matvec_fused(const WView& w, const float* x, float* y, hipStream_t s);
 hipError_t launch_block_ints(const WView& w, const AView& a, size_t m,
                              int32_t* out, hipStream_t s);
 // k_mfma.hip
