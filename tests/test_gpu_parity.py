@@ -174,10 +174,11 @@ def test_matmul_config_shapes(orc, dev, dt, k, n, m):
 
 
 @pytest.mark.parametrize("dt", [Q4K, Q6K])
-@pytest.mark.parametrize("m", [64, 130])
-def test_matmul_prefill_sizes(orc, dev, dt, m):
-    rng = np.random.default_rng(8000 + dt + m)
-    n, k = 512, 4096
+@pytest.mark.parametrize("m,n,k", [(64, 512, 4096), (130, 512, 4096), (300, 200, 768), (9, 129, 256),
+                                   (257, 384, 1280)])
+def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
+    """Prefill route (m > 8): ragged m and n against the tile sizes, 1-5 super-blocks."""
+    rng = np.random.default_rng(8000 + dt + m + n + k)
     blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
     qt = upload(blocks, n, k, dt, dev)
