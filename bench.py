@@ -43,13 +43,45 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=512)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "matvec", "prefill"], default="all")
+    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy"], default="all",
+                   help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters)")
+    p.add_argument("--eager", action="store_true",
+                   help="launch steps one by one instead of replaying a HIP graph (for counter runs)")
     return p.parse_args()
 
 
-def capture(fn, steps: int, stream):
+class Eager:
+    """Stand-in for a captured graph: `replay` launches the steps directly."""
+
+    def __init__(self, fn, steps: int):
+        self.fn, self.steps = fn, steps
+
+    def replay(self):
+        for i in range(self.steps):
+            self.fn(i)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_q4k_matvec_k4096_n14336_m1.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the matvec kernel, as recorded from the
+    FETCH_SIZE / WRITE_SIZE counter runs (scaled by the copy calibration)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def capture(fn, steps: int, stream, eager: bool = False):
     import torch
 
+    if eager:
+        return Eager(fn, steps)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for i in range(steps):
@@ -107,6 +139,20 @@ def main():
                    "weight_copies": args.copies, "parallelism": "single GPU"},
     }
 
+    if args.only == "copy":
+        nbytes = 512 << 20
+        src = torch.empty(nbytes // 4, device=dev, dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                dst.copy_(src)
+            g = capture(lambda i: dst.copy_(src), 10, stream, args.eager)
+        ms = time_graph(g, stream) / 10
+        print(json.dumps({"metric": "device copy GB/s (read + write)", "bytes_read": nbytes,
+                          "bytes_written": nbytes, "ms_per_copy": round(ms, 5),
+                          "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}), flush=True)
+        return
+
     # ---------------- weights: rotated copies, quantized on the device
     copies = []
     for _ in range(args.copies):
@@ -136,8 +182,8 @@ def main():
                 kernel_only(i)
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
-            g_step = capture(step, args.steps, stream)
-            g_kern = capture(kernel_only, args.steps, stream)
+            g_step = capture(step, args.steps, stream, args.eager)
+            g_kern = capture(kernel_only, args.steps, stream, args.eager)
         torch.cuda.synchronize()
         ms_step = time_graph(g_step, stream) / args.steps
         ms_kern = time_graph(g_kern, stream) / args.steps
@@ -155,7 +201,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.000) + WRITE_SIZE (x1.000), "
+                              "profiles/hbm_traffic_q4k_matvec_k4096_n14336_m1.md",
             "algorithmic_bytes_per_launch": algo_bytes,
             "avg_launch_us": round(ms_kern * 1e3, 3),
         }
@@ -182,8 +230,8 @@ def main():
                 pkern(i)
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
-            gp = capture(pstep, psteps, stream)
-            gk = capture(pkern, psteps, stream)
+            gp = capture(pstep, psteps, stream, args.eager)
+            gk = capture(pkern, psteps, stream, args.eager)
         ms_p = time_graph(gp, stream) / psteps
         ms_k = time_graph(gk, stream) / psteps
         ops = 2.0 * m * N_DIM * K_DIM
@@ -221,13 +269,25 @@ def main():
             times.append(time.perf_counter() - t0)
             i += 1
         med = float(np.median(times))
+        # the same calls without the activation quantization (kernel only)
+        lhs_q = oracle.quantize_lhs(oracle.Q4K, xh)
+        times_k = []
+        t_end = time.perf_counter() + args.cpu_seconds / 2
+        while time.perf_counter() < t_end or len(times_k) < 5:
+            t0 = time.perf_counter()
+            oracle.cpu_matmul_preq(oracle.Q4K, lhs_q, host_w[i % ncopies], 1, K_DIM, N_DIM)
+            times_k.append(time.perf_counter() - t0)
+            i += 1
+        med_k = float(np.median(times_k))
         result["cpu_baseline"] = {
             "value": round(algo_bytes / med / 1e9, 2),
             "unit": "GB/s",
             "cores": threads,
             "kind": "port",
+            "value_excl_quantize": round(algo_bytes / med_k / 1e9, 2),
             "sample": f"{len(times)} calls of Q4_K 4096->14336 M=1 (quantize_lhs + AVX2 vec_dot_q4k_q8k over "
-                      f"128-column tasks), {ncopies} rotated weight copies, median {med * 1e3:.3f} ms",
+                      f"128-column tasks), {ncopies} rotated weight copies, median {med * 1e3:.3f} ms; "
+                      f"value_excl_quantize: {len(times_k)} calls on pre-quantized lhs, median {med_k * 1e3:.3f} ms",
         }
 
     print(json.dumps(result), flush=True)

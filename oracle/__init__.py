@@ -177,6 +177,14 @@ def cpu_matmul(dt: int, lhs: np.ndarray, w_blocks: np.ndarray, n: int, scratch: 
     return dst
 
 
+def cpu_matmul_preq(dt: int, lhs_blocks: np.ndarray, w_blocks: np.ndarray, m: int, k: int, n: int) -> np.ndarray:
+    """The AVX2 baseline on an already-quantized lhs (threaded kernel only)."""
+    dst = np.zeros((m, n), dtype=np.float32)
+    assert lib().cpu_matmul_preq(dt, m, k, n, lhs_blocks.ctypes.data, w_blocks.ctypes.data,
+                                 dst.ctypes.data) == 0
+    return dst
+
+
 def f32_to_f16_bits(x: float) -> int:
     return lib().orc_f32_to_f16(x)
 
