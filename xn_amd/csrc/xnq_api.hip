@@ -157,7 +157,10 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
     case XNQ_Q8_0: L.q_row = L.nb * 32; L.d_row = L.nb * 2; break;
     case XNQ_Q4_0: L.q_row = L.nb * 16; L.d_row = L.nb * 2; break;
     case XNQ_Q4K: L.q_row = L.nb * 128; L.s_row = L.nb * 16; break;
-    case XNQ_Q6K: L.q_row = L.nb * 128; L.h_row = L.nb * 64; L.s_row = L.nb * 16; L.d_row = L.nb * 2; break;
+    case XNQ_Q6K:
+        // d rows padded to 4 bytes: super-block sb's f16 is half (sb & 1) of dword sb / 2
+        L.q_row = L.nb * 128; L.h_row = L.nb * 64; L.s_row = L.nb * 16; L.d_row = ((L.nb + 1) & ~size_t(1)) * 2;
+        break;
     default: *err = "unsupported dtype"; return false;
     }
     size_t off = 0;
