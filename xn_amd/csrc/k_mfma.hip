@@ -16,19 +16,25 @@
 // giving the exact integer I1 (resp. I) per super-block; the f32 epilogue then
 // applies d_a * d_w once per super-block.  The Q4K min term is a GEMM over
 // the 8 sub-blocks of a super-block with f32 operands -d_a*bsum32 and
-// dmin*m_j; it runs on the bf16 matrix cores with both operands split hi+lo
-// (three products, ~16-bit mantissa) and accumulates into the f32 output.
+// dmin*m_j, both split into bf16 hi + lo (~16 significant bits); it runs on
+// the bf16 matrix cores (two K=16 products) into the f32 output.
 //
-// Tiling: 512 threads (8 wavefronts as 4 x 2), 256 x 128 output tile, each
-// wavefront 64 x 64 = 2 x 2 v_mfma_i32_32x32x32_i8 tiles.  K advances 64 per
-// stage.  Every byte a stage needs (activation tile, raw weight chunks and
-// scales, the per-super-block epilogue operands) is fetched with
-// global_load_lds DMA straight into a 4-slot LDS ring, three stages ahead of
-// the one being multiplied, so no registers hold data in flight.  Each
-// wavefront waits only for its own DMA (s_waitcnt vmcnt with the exact count
-// of younger DMA it has issued).  A wavefront expands into the digit planes
-// exactly the weight chunks it fetched itself, so the single barrier per
-// stage publishes both the next activation tile and the next digit planes.
+// Tiling: 512 threads = 8 wavefronts, two per SIMD, as 4 x 2 over a 256 x
+// 128 output tile; each wavefront owns 64 x 64 = 2 x 2 tiles of
+// v_mfma_i32_32x32x32_i8 (192 accumulator registers: two int32 digit sums
+// and the f32 output).  K advances 64 per stage.  Every byte a stage needs
+// (activation tile, raw weight chunks, once per super-block d_a, bsums and
+// block headers) is fetched with global_load_lds DMA straight into a 4-slot
+// LDS ring three stages ahead, one DMA instruction at a time between MFMAs,
+// so a DMA issue that the memory pipeline holds back does not idle the
+// matrix core.  The wavefronts come in two groups of four (one of each per
+// SIMD): group 0 fetches and expands the weights (weight chunks -> int8
+// digit planes, block headers -> the column-side min-term operand), group 1
+// fetches the per-super-block activation data (d_a, bsums -> the row-side
+// min-term operand); both fetch activation tiles.  Each wavefront waits only
+// for its own DMA (s_waitcnt vmcnt with the exact count of younger DMA it has
+// issued) and processes only data it fetched itself, so one barrier per stage
+// publishes both the next activation tile and the next digit planes.
 #include <type_traits>
 
 #include "xnq_device.h"
@@ -46,7 +52,7 @@ typedef short v2s __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 256, kBN = 128;
 constexpr int kWaves = 8, kThreads = kWaves * 64;
-constexpr int kTM = 2, kTN = 2;  // 32x32 tiles per wavefront
+constexpr int kTM = 2, kTN = 2;  // 32x32 tiles per wavefront (64 x 64)
 constexpr int kRing = 4;         // LDS ring slots (3 stages in flight + the current one)
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -54,9 +60,9 @@ typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
 // LDS map (bytes).  Per stage: activation tile, raw weight chunks (Q6K: and
 // their high bits).  Per super-block (two buffers, by parity): d_a; Q4K: the
-// bsum pairs, turned in place into the min-term operand; the 16-byte block
-// header (Q4K: d, dmin, scales; Q6K: the int8 scales); Q4K: the weight-side
-// min-term operand, Q6K: the d dword.
+// bsum pairs, turned in place into the row-side min-term operand; the
+// 16-byte block header (Q4K: d, dmin, scales; Q6K: the int8 scales); Q4K:
+// the column-side min-term operand, Q6K: the d dword.
 template <int DT>
 struct Lay {
     static constexpr bool kQ4K = DT == XNQ_Q4K;
@@ -76,10 +82,12 @@ struct Lay {
     static constexpr int kOffEpi = kOffPlanes + 2 * kPlanes;
     static constexpr int kLds = kOffEpi + 2 * kEpi;
     static_assert(kLds <= 160 * 1024, "LDS budget");
-    // DMA instructions one wavefront issues per stage, and the extra ones at
-    // a super-block's first stage (d_a, bsums or scales, header or d)
-    static constexpr int kBase = kQ4K ? 3 : 4;
-    static constexpr int kExtra = 3;
+    // DMA instructions per stage of a group-0 / group-1 wavefront, and the
+    // extra ones at a super-block's first stage
+    static constexpr int kBase0 = kQ4K ? 3 : 4;   // 2 activation pieces, chunks, Q6K qh
+    static constexpr int kExtra0 = kQ4K ? 1 : 2;  // header (Q6K scales), Q6K d
+    static constexpr int kBase1 = 2;              // 2 activation pieces
+    static constexpr int kExtra1 = kQ4K ? 3 : 1;  // d_a, Q4K 2 x bsums
 };
 
 // global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
@@ -95,7 +103,7 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t ld
                  : "memory");
 }
 // Wait until at most n of this wavefront's vector memory operations are
-// outstanding (n is wavefront-uniform; counts above 15 wait for all).
+// outstanding (n is wavefront-uniform; counts above 31 wait for all).
 __device__ __forceinline__ void wait_vmcnt(int n) {
     switch (n) {
 #define XNQ_W(N)                                              \
@@ -103,16 +111,28 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
         asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
         break;
         XNQ_W(1) XNQ_W(2) XNQ_W(3) XNQ_W(4) XNQ_W(5) XNQ_W(6) XNQ_W(7) XNQ_W(8)
-        XNQ_W(9) XNQ_W(10) XNQ_W(11) XNQ_W(12) XNQ_W(13) XNQ_W(14) XNQ_W(15)
+        XNQ_W(9) XNQ_W(10) XNQ_W(11) XNQ_W(12) XNQ_W(13) XNQ_W(14) XNQ_W(15) XNQ_W(16)
+        XNQ_W(17) XNQ_W(18) XNQ_W(19) XNQ_W(20) XNQ_W(21) XNQ_W(22) XNQ_W(23) XNQ_W(24)
+        XNQ_W(25) XNQ_W(26) XNQ_W(27) XNQ_W(28) XNQ_W(29) XNQ_W(30) XNQ_W(31)
 #undef XNQ_W
     default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
 
-// bytes of d (each <= 15) times s (<= 7); no product leaves its byte
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+
+// bytes of d (each <= 15) times s (<= 7): every product is <= 105, so no
+// carry leaves its byte and one packed 16-bit multiply does all four
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
-    const uint32_t a = d & 0x00FF00FFu, b = (d >> 8) & 0x00FF00FFu;
-    return __umul24(a, s) | (__umul24(b, s) << 8);
+    const v2u16 s2 = {(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, d) * s2);
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale.
@@ -129,14 +149,18 @@ __device__ __forceinline__ void q6_digits(uint32_t q, int sc, uint32_t& lo, uint
     hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
 }
 
-// v = hi + lo with hi = bf16(v), lo = bf16(v - hi): ~16 significant bits
-__device__ __forceinline__ void bf16_split(float v, __bf16& h, __bf16& l) {
-    h = (__bf16)v;
-    l = (__bf16)(v - (float)h);
+// 4 floats -> bf16 hi | bf16 lo (v = hi + lo to ~16 significant bits), packed as 16 bytes
+__device__ __forceinline__ uint4 bf16_split4(const float* v) {
+    v4bf h, l;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const __bf16 hb = (__bf16)v[t];
+        h[t] = hb;
+        l[t] = (__bf16)(v[t] - (float)hb);
+    }
+    const uint2 hu = __builtin_bit_cast(uint2, h), lu = __builtin_bit_cast(uint2, l);
+    return make_uint4(hu.x, hu.y, lu.x, lu.y);
 }
-
-template <int N>
-using ic = std::integral_constant<int, N>;
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_t m, float* __restrict__ y) {
@@ -147,131 +171,18 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave >> 1, wn = wave & 1;  // 4 x 2 wavefronts, 64 x 64 each
     const uint32_t m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-    const uint32_t K = w.k, nsb = K / 256, nstage = 4 * nsb;
+    const uint32_t K = w.k, nsb = K / 256;
     const ActImg& A = a.A;
     const uint32_t lbase = (uint32_t)(uintptr_t)lds;  // low half of the flat address = LDS offset
     const uint32_t lrow = lane & 31, lgrp = lane >> 5;
 
-    // ---- this wavefront's DMA streams (byte offsets of stage / super-block 0) ----
-    // activation pieces t = 2*wave + {0,1}: (ks, h, 64-row block)
-    uint32_t a_off[2], a_lds[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t t = 2 * wave + i, ks = t >> 3, h = (t >> 2) & 1, rb = t & 3;
-        const uint32_t row = min(m0 + rb * 64 + lane, m - 1);
-        a_off[i] = row * A.row_bytes + h * (K / 2) + ks * 16;
-        a_lds[i] = ((ks * 2 + h) * kBM + rb * 64) * 16;
-    }
-    // weights: chunk bc = wave & 1 of each stage, columns cb*32 .. +31
-    // (cb = wave >> 1); lanes 32-63 mirror lanes 0-31 and issue no DMA
-    const uint32_t bc = wave & 1, cb = wave >> 1;
-    const uint32_t bn = cb * 32 + lrow;
-    const uint32_t ncol = min(n0 + bn, w.n - 1);  // clamped: edge tiles read a valid row
-    const bool lo_half = lane < 32;
-    const uint32_t q_off = ncol * w.q_row + bc * 16;
-    const uint32_t da_off = min(m0 + 32 * wave + lrow, m - 1) * A.row_bytes + A.d_off;
-    const uint32_t sum_off = min(m0 + 32 * wave + (lane >> 1), m - 1) * A.row_bytes + A.s_off + (lane & 1) * 16;
-
-    auto count = [&](uint32_t st) -> int {
-        if (st >= nstage) return 0;
-        return L::kBase + ((st & 3) == 0 ? L::kExtra : 0);
-    };
+    // Every DMA instruction is issued by the whole wavefront (the vmcnt
+    // bookkeeping counts instructions): lanes past the last row or column
+    // re-read the last one, and those outputs are dropped at the store.
+    const uint32_t row_max = m - 1 - m0, col_max = w.n - 1 - n0;
+    auto a_row = [&](uint32_t r) { return min(r, row_max) * A.row_bytes; };  // byte offset of tile row r
+    const uint8_t* a_img = a.img + (size_t)m0 * A.row_bytes;
     auto epi_base = [&](uint32_t sb) -> uint8_t* { return lds + L::kOffEpi + (sb & 1) * L::kEpi; };
-    auto issue = [&](uint32_t st) {
-        if (st >= nstage) return;
-        const uint32_t slot = st % kRing, sb = st >> 2;
-        const uint32_t abase = lbase + L::kOffA + slot * L::kASlot;
-#pragma unroll
-        for (int i = 0; i < 2; i++) dma16(a.img, a_off[i] + st * 32, abase + a_lds[i]);
-        const uint32_t raw = lbase + L::kOffRaw + slot * L::kRawSlot + (bc * kBN + cb * 32) * 16;
-        if (lo_half) {
-            dma16(w.q, q_off + st * 32, raw);
-            if (!kQ4K) dma16(w.h, ((q_off - bc * 16) >> 1) + st * 16, raw + L::kQSlot);  // qh of chunks 2st, 2st+1
-        }
-        if ((st & 3) == 0) {
-            const uint32_t epi = lbase + L::kOffEpi + (sb & 1) * L::kEpi;
-            if (lo_half) {
-                dma4(a.img, da_off + sb * 4, epi + L::kEDa + 32 * wave * 4);
-                dma16(w.s, ncol * w.s_row + sb * 16, epi + L::kEHdr + cb * 32 * 16);
-                if (!kQ4K) dma4(w.d, ncol * w.d_row + (sb & ~1u) * 2, epi + L::kEB + cb * 32 * 4);
-            }
-            if (kQ4K) dma16(a.img, sum_off + sb * 32, epi + L::kESum + 32 * wave * 32);
-        }
-    };
-
-    // ---- this wavefront's weight chunks of stage st -> digit planes (st & 1);
-    //      at a super-block's first stage also the min-term operands of its rows/columns ----
-    auto expand = [&](uint32_t st) {
-        const uint8_t* raw = lds + L::kOffRaw + (st % kRing) * L::kRawSlot;
-        uint8_t* epi = epi_base(st >> 2);
-        const uint4 rq = *reinterpret_cast<const uint4*>(raw + (bc * kBN + bn) * 16);
-        const uint4 hd = *reinterpret_cast<const uint4*>(epi + L::kEHdr + bn * 16);
-        uint32_t p0[4], p1[4];  // high digit, low digit; 16 elements each
-        if (kQ4K) {
-            int sc, mn;
-            q4k_scale_min(hd.y, hd.z, hd.w, (int)((2 * st + bc) & 7), sc, mn);
-            const uint32_t sh = (uint32_t)sc >> 3, sl = (uint32_t)sc & 7;
-            const uint32_t q4[4] = {rq.x, rq.y, rq.z, rq.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t nib = lgrp ? ((q4[j] >> 4) & 0x0F0F0F0Fu) : (q4[j] & 0x0F0F0F0Fu);
-                p0[j] = mul_bytes(nib, sh);
-                p1[j] = mul_bytes(nib, sl);
-            }
-            if ((st & 3) == 0) {
-                // rows: -d_a * bsum32 of 4 sub-blocks, split to bf16 hi|lo, in place
-                int4* sp = reinterpret_cast<int4*>(epi + L::kESum + 32 * wave * 32) + lane;
-                const int4 pr = *sp;
-                const float da = reinterpret_cast<const float*>(epi + L::kEDa)[32 * wave + (lane >> 1)];
-                const int32_t prs[4] = {pr.x, pr.y, pr.z, pr.w};
-                v4bf h4, l4;
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const int bs = (int)(int16_t)(prs[t] & 0xffff) + (int)(int16_t)(prs[t] >> 16);
-                    __bf16 hh, ll;
-                    bf16_split(-da * (float)bs, hh, ll);
-                    h4[t] = hh;
-                    l4[t] = ll;
-                }
-                uint4 o;
-                o.x = __builtin_bit_cast(uint2, h4).x;
-                o.y = __builtin_bit_cast(uint2, h4).y;
-                o.z = __builtin_bit_cast(uint2, l4).x;
-                o.w = __builtin_bit_cast(uint2, l4).y;
-                *reinterpret_cast<uint4*>(sp) = o;
-                if (lo_half) {
-                    // columns: dmin * m_j of sub-blocks 4*bc .. 4*bc+3, bf16 hi|lo
-                    const float dm = f16_bits_to_f32(hd.x >> 16);
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        int sc2, mn2;
-                        q4k_scale_min(hd.y, hd.z, hd.w, (int)(4 * bc + t), sc2, mn2);
-                        __bf16 hh, ll;
-                        bf16_split(dm * (float)mn2, hh, ll);
-                        h4[t] = hh;
-                        l4[t] = ll;
-                    }
-                    o.x = __builtin_bit_cast(uint2, h4).x;
-                    o.y = __builtin_bit_cast(uint2, h4).y;
-                    o.z = __builtin_bit_cast(uint2, l4).x;
-                    o.w = __builtin_bit_cast(uint2, l4).y;
-                    *reinterpret_cast<uint4*>(epi + L::kEB + (bn * 2 + bc) * 16) = o;
-                }
-            }
-        } else {
-            const uint2 qh = *reinterpret_cast<const uint2*>(raw + L::kQSlot + (bc * kBN + bn) * 16 + bc * 8);
-            int b[8];
-            q6k_unpack(rq, qh, b);
-            const uint32_t q = st & 3;  // scales of chunks 2st, 2st+1
-            const uint32_t sw = q == 0 ? hd.x : (q == 1 ? hd.y : (q == 2 ? hd.z : hd.w));
-            const int sc = (int)(int8_t)(sw >> (8 * (2 * bc + lgrp)));
-#pragma unroll
-            for (int j = 0; j < 4; j++) q6_digits((uint32_t)b[4 * lgrp + j], sc, p1[j], p0[j]);
-        }
-        uint8_t* pl = lds + L::kOffPlanes + (st & 1) * L::kPlanes;
-        *reinterpret_cast<uint4*>(pl + (((bc * 2 + 0) * 2 + lgrp) * kBN + bn) * 16) = make_uint4(p0[0], p0[1], p0[2], p0[3]);
-        *reinterpret_cast<uint4*>(pl + (((bc * 2 + 1) * 2 + lgrp) * kBN + bn) * 16) = make_uint4(p1[0], p1[1], p1[2], p1[3]);
-    };
 
     v16f accf[kTM][kTN];
     v16i hi[kTM][kTN], lo[kTM][kTN];
@@ -282,94 +193,220 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
 
     // ---- super-block epilogue of tile (i, j): y += d_a d_w (hi * 2^s + lo) [- d_a dmin I2] ----
     constexpr int kShift = kQ4K ? 3 : 7;
-    auto tile_dw = [&](uint32_t sb, int j) -> float {
+    auto epilogue_tile = [&](uint32_t sb, int i, int j) {
         const uint8_t* epi = epi_base(sb);
+        const float* eda = reinterpret_cast<const float*>(epi + L::kEDa);
         const uint32_t nl = wn * 64 + j * 32 + lrow;
-        if (kQ4K) return f16_bits_to_f32(*reinterpret_cast<const uint32_t*>(epi + L::kEHdr + nl * 16) & 0xffffu);
-        // d rows are padded to 4 bytes, so the dword holds super-blocks 2*(sb/2), +1
-        const uint32_t dd = reinterpret_cast<const uint32_t*>(epi + L::kEB)[nl];
-        return f16_bits_to_f32((sb & 1) ? (dd >> 16) : (dd & 0xffffu));
-    };
-    auto epilogue_tile = [&](uint32_t sb, int i, int j, float dw, const float* da) {
+        float dw;
+        if (kQ4K) {
+            dw = f16_bits_to_f32(*reinterpret_cast<const uint32_t*>(epi + L::kEHdr + nl * 16) & 0xffffu);
+        } else {
+            // d rows are padded to 4 bytes: the dword holds super-blocks 2*(sb/2), +1
+            const uint32_t dd = reinterpret_cast<const uint32_t*>(epi + L::kEB)[nl];
+            dw = f16_bits_to_f32((sb & 1) ? (dd >> 16) : (dd & 0xffffu));
+        }
+        const uint32_t rl = wm * 64 + i * 32;
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int iv = hi[i][j][e] * (1 << kShift) + lo[i][j][e];
-            accf[i][j][e] = fmaf((float)iv, dw * da[e], accf[i][j][e]);
+        for (int q = 0; q < 4; q++) {
+            const float4 d4 = *reinterpret_cast<const float4*>(eda + rl + q * 8 + lgrp * 4);
+            const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int iv = hi[i][j][4 * q + e] * (1 << kShift) + lo[i][j][4 * q + e];
+                accf[i][j][4 * q + e] = fmaf((float)iv, dw * da[e], accf[i][j][4 * q + e]);
+            }
         }
         if (kQ4K) {
-            const uint8_t* epi = epi_base(sb);
-            const uint4 av = reinterpret_cast<const uint4*>(epi + L::kESum)[(wm * 64 + i * 32 + lrow) * 2 + lgrp];
-            const uint4 bv = reinterpret_cast<const uint4*>(epi + L::kEB)[(wn * 64 + j * 32 + lrow) * 2 + lgrp];
+            const uint4 bmin = reinterpret_cast<const uint4*>(epi + L::kEB)[nl * 2 + lgrp];
+            const uint4 av = reinterpret_cast<const uint4*>(epi + L::kESum)[(rl + lrow) * 2 + lgrp];
             const v8bf a8 = __builtin_bit_cast(v8bf, av);
-            const v8bf bh8 = __builtin_bit_cast(v8bf, make_uint4(bv.x, bv.y, bv.x, bv.y));
-            const v8bf bl8 = __builtin_bit_cast(v8bf, make_uint4(bv.z, bv.w, bv.z, bv.w));
+            const v8bf bh8 = __builtin_bit_cast(v8bf, make_uint4(bmin.x, bmin.y, bmin.x, bmin.y));
+            const v8bf bl8 = __builtin_bit_cast(v8bf, make_uint4(bmin.z, bmin.w, bmin.z, bmin.w));
             accf[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bh8, accf[i][j], 0, 0, 0);
             accf[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bl8, accf[i][j], 0, 0, 0);
         }
     };
-    auto load_da = [&](uint32_t sb, int i, float* da) {
-        const float* ep = reinterpret_cast<const float*>(epi_base(sb) + L::kEDa);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 d4 = *reinterpret_cast<const float4*>(ep + wm * 64 + i * 32 + q * 8 + lgrp * 4);
-            da[4 * q + 0] = d4.x;
-            da[4 * q + 1] = d4.y;
-            da[4 * q + 2] = d4.z;
-            da[4 * q + 3] = d4.w;
-        }
-    };
 
-    auto epilogue = [&](uint32_t sb) {
-#pragma unroll
-        for (int j = 0; j < kTN; j++) {
-            const float dw = tile_dw(sb, j);
-#pragma unroll
-            for (int i = 0; i < kTM; i++) {
-                float da[16];
-                load_da(sb, i, da);
-                epilogue_tile(sb, i, j, dw, da);
+    // The main loop, specialised per wavefront group (G = 0: weights, 1: activation side data).
+    auto run = [&](auto gc) {
+        constexpr int G = decltype(gc)::value;
+        constexpr int kBase = G == 0 ? L::kBase0 : L::kBase1;
+        constexpr int kExtra = G == 0 ? L::kExtra0 : L::kExtra1;
+        constexpr int kParts = kBase + kExtra;
+        const uint32_t gw = wave & 3;                  // index within the group
+        const uint32_t bc = gw >> 1, cw = gw & 1;      // group 0: chunk and 64-column half
+        const uint32_t col = cw * 64 + lane;           // group 0: this lane's weight column
+        const uint32_t q_lane = min(col, col_max) * w.q_row;
+        const uint8_t* wq = w.q + (size_t)n0 * w.q_row;
+        const uint8_t* wh = w.h + (size_t)n0 * w.h_row;
+        const uint8_t* ws = w.s + (size_t)n0 * w.s_row;
+        const uint8_t* wd = w.d + (size_t)n0 * w.d_row;
+        const uint32_t nstage = 4 * nsb;
+
+        // DMA instruction p of stage st (parts past kBase only at a super-block's first stage)
+        auto issue_part = [&](uint32_t st, int p) {
+            const uint32_t slot = st % kRing, sb = st >> 2;
+            const uint32_t epi = lbase + L::kOffEpi + (sb & 1) * L::kEpi;
+            if (p < 2) {
+                // activation piece t = 2*wave + p: (ks, h, 64-row block)
+                const uint32_t t = 2 * wave + p, ks = t >> 3, h = (t >> 2) & 1, rb = t & 3;
+                dma16(a_img + h * (K / 2) + ks * 16 + st * 32, a_row(rb * 64 + lane),
+                      lbase + L::kOffA + slot * L::kASlot + ((ks * 2 + h) * kBM + rb * 64) * 16);
+                return;
             }
-        }
-    };
+            if (G == 0) {
+                const uint32_t raw = lbase + L::kOffRaw + slot * L::kRawSlot + (bc * kBN + cw * 64) * 16;
+                if (p == 2) dma16(wq + bc * 16 + st * 32, q_lane, raw);
+                if (!kQ4K && p == 3) dma16(wh + st * 16, q_lane >> 1, raw + L::kQSlot);  // qh of chunks 2st, 2st+1
+                if (p == kBase) dma16(ws + sb * 16, q_lane >> 3, epi + L::kEHdr + cw * 64 * 16);
+                if (!kQ4K && p == kBase + 1)
+                    dma4(wd + (sb & ~1u) * 2, min(col, col_max) * w.d_row, epi + L::kEB + cw * 64 * 4);
+            } else {
+                if (p == kBase) dma4(a_img + A.d_off + sb * 4, a_row(64 * gw + lane), epi + L::kEDa + 64 * gw * 4);
+                if (kQ4K && p > kBase) {
+                    const uint32_t i = p - kBase - 1;  // rows 64*gw + 32*i + lane/2
+                    dma16(a_img + A.s_off + sb * 32, a_row(64 * gw + 32 * i + (lane >> 1)) + (lane & 1) * 16,
+                          epi + L::kESum + (64 * gw + 32 * i) * 32);
+                }
+            }
+        };
 
-    // ---- one stage: 2 chunks x 2 x 2 tiles x 2 digit planes of int8 MFMA.  At a
-    //      super-block's first stage the sums start from zero; its last stage
-    //      ends with the super-block's epilogue ----
-    auto stage = [&](uint32_t sb, auto tc) {
-        constexpr int t = decltype(tc)::value;
-        const uint32_t s = 4 * sb + t;
-        issue(s + 3);
-        const uint8_t* abase = lds + L::kOffA + (s % kRing) * L::kASlot;
-        const uint8_t* pbase = lds + L::kOffPlanes + (s & 1) * L::kPlanes;
+        // Stage st's own-data work after its DMA has landed: group 0 turns its
+        // weight chunks into digit planes (st & 1) and, at a super-block's first
+        // stage, its columns' block headers into the min-term operand; group 1
+        // turns its rows' bsums into the min-term operand at a first stage.
+        auto expand = [&](uint32_t st, auto firstc) {
+            constexpr bool kFirst = decltype(firstc)::value;
+            uint8_t* epi = epi_base(st >> 2);
+            if (G == 1) {
+                if (kQ4K && kFirst) {
+                    const float* eda = reinterpret_cast<const float*>(epi + L::kEDa);
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            auto a_frag = [&](int i) {
+                    for (int i = 0; i < 2; i++) {
+                        uint4* sp = reinterpret_cast<uint4*>(epi + L::kESum + (64 * gw + 32 * i) * 32) + lane;
+                        const uint4 pr = *sp;
+                        const float da = eda[64 * gw + 32 * i + (lane >> 1)];
+                        const uint32_t prs[4] = {pr.x, pr.y, pr.z, pr.w};
+                        float v[4];
+#pragma unroll
+                        for (int t = 0; t < 4; t++)
+                            v[t] = -da * (float)((int)(int16_t)(prs[t] & 0xffffu) + (int)(int16_t)(prs[t] >> 16));
+                        *sp = bf16_split4(v);
+                    }
+                }
+                return;
+            }
+            const uint8_t* raw = lds + L::kOffRaw + (st % kRing) * L::kRawSlot;
+            const uint4 rq = *reinterpret_cast<const uint4*>(raw + (bc * kBN + col) * 16);
+            const uint4 hd = *reinterpret_cast<const uint4*>(epi + L::kEHdr + col * 16);
+            uint8_t* pl = lds + L::kOffPlanes + (st & 1) * L::kPlanes;
+            auto put = [&](int plane, int half, uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3) {
+                *reinterpret_cast<uint4*>(pl + (((bc * 2 + plane) * 2 + half) * kBN + col) * 16) = make_uint4(x0, x1, x2, x3);
+            };
+            if (kQ4K) {
+                int sc, mn;
+                q4k_scale_min(hd.y, hd.z, hd.w, (int)((2 * st + bc) & 7), sc, mn);
+                const uint32_t sh = (uint32_t)sc >> 3, sl = (uint32_t)sc & 7;
+                const uint32_t q4[4] = {rq.x, rq.y, rq.z, rq.w};
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    uint32_t nib[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) nib[j] = (q4[j] >> (4 * half)) & 0x0F0F0F0Fu;
+                    put(0, half, mul_bytes(nib[0], sh), mul_bytes(nib[1], sh), mul_bytes(nib[2], sh), mul_bytes(nib[3], sh));
+                    put(1, half, mul_bytes(nib[0], sl), mul_bytes(nib[1], sl), mul_bytes(nib[2], sl), mul_bytes(nib[3], sl));
+                }
+                if (kFirst) {
+                    // this column: dmin * m_j of sub-blocks 4*bc .. 4*bc+3 -> bf16 hi|lo
+                    const float dm = f16_bits_to_f32(hd.x >> 16);
+                    float v[4];
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        int sc2, mn2;
+                        q4k_scale_min(hd.y, hd.z, hd.w, (int)(4 * bc + t), sc2, mn2);
+                        v[t] = dm * (float)mn2;
+                    }
+                    *reinterpret_cast<uint4*>(epi + L::kEB + (col * 2 + bc) * 16) = bf16_split4(v);
+                }
+            } else {
+                const uint2 qh = *reinterpret_cast<const uint2*>(raw + L::kQSlot + (bc * kBN + col) * 16 + bc * 8);
+                int b[8];
+                q6k_unpack(rq, qh, b);
+                const uint32_t q = st & 3;  // scales of chunks 2st, 2st+1
+                const uint32_t sw = q == 0 ? hd.x : (q == 1 ? hd.y : (q == 2 ? hd.z : hd.w));
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const int sc = (int)(int8_t)(sw >> (8 * (2 * bc + half)));
+                    uint32_t lo4[4], hi4[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) q6_digits((uint32_t)b[4 * half + j], sc, lo4[j], hi4[j]);
+                    put(0, half, hi4[0], hi4[1], hi4[2], hi4[3]);
+                    put(1, half, lo4[0], lo4[1], lo4[2], lo4[3]);
+                }
+            }
+        };
+
+        // ---- one stage s = 4*sb + t: 2 chunks x 2 x 2 tiles x 2 digit planes of
+        //      int8 MFMA.  Chunk 0 issues stage s+3's DMA between its MFMAs and,
+        //      at a super-block's first stage, starts the sums from zero.  Chunk
+        //      1's MFMAs are interleaved with stage s+1's expansion.  A
+        //      super-block's last stage ends with its epilogue.  kLast marks the
+        //      final super-block, where stages past the end are neither fetched
+        //      nor expanded ----
+        auto stage = [&](uint32_t sb, auto tc, auto lastc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr bool kLast = decltype(lastc)::value != 0;
+            constexpr bool kMore = !kLast || t == 0;      // stage s+3 exists
+            constexpr bool kExpand = !kLast || t < 3;     // stage s+1 exists
+            constexpr bool kFirst3 = ((t + 3) & 3) == 0;  // stage s+3 starts a super-block
+            constexpr int kNParts = kFirst3 ? kParts : kBase;
+            // this wavefront's DMA still in flight once stage s+1's has landed
+            constexpr int kC2 = (kLast && t >= 2) ? 0 : kBase + (t == 2 ? kExtra : 0);
+            constexpr int kC3 = kMore ? kBase + (kFirst3 ? kExtra : 0) : 0;
+            const uint32_t s = 4 * sb + t;
+            const uint8_t* abase = lds + L::kOffA + t * L::kASlot;  // slot s % 4 = t
+            const uint8_t* pbase = lds + L::kOffPlanes + (t & 1) * L::kPlanes;
+            auto a_frag = [&](int ks, int i) {
                 return *reinterpret_cast<const v4i*>(abase + ((ks * 2 + lgrp) * kBM + wm * 64 + i * 32 + lrow) * 16);
             };
-            auto b_frag = [&](int p, int j) {
+            auto b_frag = [&](int ks, int p, int j) {
                 return *reinterpret_cast<const v4i*>(
                     pbase + (((ks * 2 + p) * 2 + lgrp) * kBN + wn * 64 + j * 32 + lrow) * 16);
             };
-            v4i av[kTM];
+            {
+                v4i av[kTM], bv[2][kTN];
 #pragma unroll
-            for (int i = 0; i < kTM; i++) av[i] = a_frag(i);
-            if (t == 0 && ks == 0) {
-                // a super-block's first chunk: the sums start from zero
-#pragma unroll
-                for (int j = 0; j < kTN; j++) {
-                    const v4i b0 = b_frag(0, j), b1 = b_frag(1, j);
-#pragma unroll
-                    for (int i = 0; i < kTM; i++) {
-                        hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], b0, v16i{}, 0, 0, 0);
-                        lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], b1, v16i{}, 0, 0, 0);
-                    }
-                }
-            } else {
-                v4i bv[2][kTN];
+                for (int i = 0; i < kTM; i++) av[i] = a_frag(0, i);
 #pragma unroll
                 for (int p = 0; p < 2; p++)
 #pragma unroll
-                    for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(p, j);
+                    for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(0, p, j);
+#pragma unroll
+                for (int i = 0; i < kTM; i++)
+#pragma unroll
+                    for (int j = 0; j < kTN; j++) {
+                        const int k = (i * kTN + j) * 2;
+                        if (t == 0) {
+                            hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[0][j], v16i{}, 0, 0, 0);
+                            lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[1][j], v16i{}, 0, 0, 0);
+                        } else {
+                            hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[0][j], hi[i][j], 0, 0, 0);
+                            lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[1][j], lo[i][j], 0, 0, 0);
+                        }
+                        if (kMore && k < kNParts) issue_part(s + 3, k);
+                        if (kMore && k + 1 < kNParts) issue_part(s + 3, k + 1);
+                    }
+            }
+            if (kExpand) wait_vm<kC2 + kC3>();
+            {
+                v4i av[kTM], bv[2][kTN];
+#pragma unroll
+                for (int i = 0; i < kTM; i++) av[i] = a_frag(1, i);
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+#pragma unroll
+                    for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(1, p, j);
+                if (kExpand) expand(s + 1, std::integral_constant<bool, ((t + 1) & 3) == 0>{});
 #pragma unroll
                 for (int i = 0; i < kTM; i++)
 #pragma unroll
@@ -377,31 +414,57 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                         hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[0][j], hi[i][j], 0, 0, 0);
                         lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[1][j], lo[i][j], 0, 0, 0);
                     }
+                // interleave: LDS reads first, then one MFMA per few VALU
+                // instructions of the expansion, then its LDS writes
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+                for (int k = 0; k < 2 * kTM * kTN; k++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
             }
-            // the next stage's digit planes, while this chunk's MFMAs run
-            if (ks == 0 && s + 1 < nstage) {
-                wait_vmcnt(count(s + 2) + count(s + 3));
-                expand(s + 1);
+            if (t == 3) {
+#pragma unroll
+                for (int i = 0; i < kTM; i++)
+#pragma unroll
+                    for (int j = 0; j < kTN; j++) epilogue_tile(sb, i, j);
             }
-        }
-        if (t == 3) epilogue(sb);
+            __syncthreads();
+        };
+
+        // prologue: stages 0-2 in flight, stage 0 expanded and published
+#pragma unroll
+        for (int p = 0; p < kParts; p++) issue_part(0, p);
+        if (nstage > 1)
+#pragma unroll
+            for (int p = 0; p < kBase; p++) issue_part(1, p);
+        if (nstage > 2)
+#pragma unroll
+            for (int p = 0; p < kBase; p++) issue_part(2, p);
+        wait_vm<0>();
+        expand(0, std::true_type{});
         __syncthreads();
+
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        for (uint32_t sb = 0; sb + 1 < nsb; sb++) {
+            stage(sb, I0{}, std::false_type{});
+            stage(sb, I1{}, std::false_type{});
+            stage(sb, I2{}, std::false_type{});
+            stage(sb, I3{}, std::false_type{});
+        }
+        stage(nsb - 1, I0{}, std::true_type{});
+        stage(nsb - 1, I1{}, std::true_type{});
+        stage(nsb - 1, I2{}, std::true_type{});
+        stage(nsb - 1, I3{}, std::true_type{});
     };
-
-    // prologue: stages 0-2 in flight, stage 0 expanded and published
-    issue(0);
-    issue(1);
-    issue(2);
-    wait_vmcnt(count(1) + count(2));
-    expand(0);
-    __syncthreads();
-
-    for (uint32_t sb = 0; sb < nsb; sb++) {
-        stage(sb, ic<0>{});
-        stage(sb, ic<1>{});
-        stage(sb, ic<2>{});
-        stage(sb, ic<3>{});
-    }
+    if (wave < 4)
+        run(std::integral_constant<int, 0>{});
+    else
+        run(std::integral_constant<int, 1>{});
 
     // ---- write the tile ----
 #pragma unroll
