@@ -9,6 +9,31 @@
 
 namespace xnq {
 
+// Cross-lane steps on the DPP path (no LDS round trip).  Controls:
+// quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror = 0x141,
+// row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v)));
+}
+
+// Largest value over the wavefront of a non-negative (or NaN) float: lanes
+// shifted in from outside a row read 0, and fmaxf drops NaN like the
+// reference's strict `amax < |x|` comparison does.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = fmaxf(v, dpp_f<0x111>(v));
+    v = fmaxf(v, dpp_f<0x112>(v));
+    v = fmaxf(v, dpp_f<0x114>(v));
+    v = fmaxf(v, dpp_f<0x118>(v));
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v));
+    v = fmaxf(v, dpp_f<0x143, 0xc>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // One 256-element Q8_K block per wavefront, elements 4*lane .. 4*lane+3 in `v`.
 struct Q8KLane {
     uint32_t packed;  // this lane's 4 quants, little-endian bytes
@@ -18,41 +43,37 @@ struct Q8KLane {
 
 __device__ __forceinline__ Q8KLane q8k_quant_wave(float4 v, int lane) {
 #pragma clang fp contract(off)
+    (void)lane;
     const float xs[4] = {v.x, v.y, v.z, v.w};
-    // Largest |x|, first index on ties (the reference's strict `amax < |x|`).
-    float amax = 0.0f, max = 0.0f;
-    int idx = 0x7fffffff;
+    // Largest |x|; the reference keeps the first index on ties (strict
+    // `amax < |x|`), so its signed value is taken from the lowest lane, and
+    // the lowest element in that lane, holding an |x| equal to the maximum.
+    float lmax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float a = fabsf(xs[i]);
-        if (amax < a) {
-            amax = a;
-            max = xs[i];
-            idx = lane * 4 + i;
-        }
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float oa = __shfl_xor(amax, off);
-        const int oi = __shfl_xor(idx, off);
-        const float om = __shfl_xor(max, off);
-        if ((oa > amax) || (oa == amax && oi < idx)) {
-            amax = oa;
-            idx = oi;
-            max = om;
-        }
-    }
+    for (int i = 0; i < 4; i++) lmax = fmaxf(lmax, fabsf(xs[i]));
+    const float amax = wave_max_nonneg(lmax);
     int8_t q[4] = {0, 0, 0, 0};
     float d = 0.0f;
     if (amax != 0.0f) {
+        float cand = 0.0f;
+        bool hit = false;
+#pragma unroll
+        for (int i = 3; i >= 0; i--)
+            if (fabsf(xs[i]) == amax) {
+                cand = xs[i];
+                hit = true;
+            }
+        const unsigned long long mask = __ballot(hit);
+        const int first = __builtin_ctzll(mask);
+        const float max = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), first));
         const float iscale = -128.0f / max;
 #pragma unroll
         for (int i = 0; i < 4; i++) q[i] = f_as_i8(fminf(roundf(iscale * xs[i]), 127.0f));
         d = 1.0f / iscale;
     }
     int s = (int)q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s += dpp_i<0xB1>(s);
+    s += dpp_i<0x4E>(s);
     Q8KLane r;
     r.packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
                ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
@@ -73,17 +94,17 @@ __device__ __forceinline__ Q80Lane q80_quant_8lanes(float4 v) {
 #pragma clang fp contract(off)
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, 0.0f);
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));
+    amax = fmaxf(amax, dpp_f<0x141>(amax));
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int8_t q0 = f_as_i8(roundf(v.x * id)), q1 = f_as_i8(roundf(v.y * id)),
                  q2 = f_as_i8(roundf(v.z * id)), q3 = f_as_i8(roundf(v.w * id));
     int s = (int)q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    s += dpp_i<0xB1>(s);
+    s += dpp_i<0x4E>(s);
+    s += dpp_i<0x141>(s);
     Q80Lane r;
     r.packed = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) | ((uint32_t)(uint8_t)q2 << 16) |
                ((uint32_t)(uint8_t)q3 << 24);
