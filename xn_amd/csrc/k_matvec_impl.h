@@ -142,27 +142,42 @@ struct Chunk {
 
 // Byte offsets are 32-bit (every plane is < 4 GiB, checked at upload), so the
 // loads use a uniform 64-bit base plus one VGPR offset.
+// Weight stream loads: each weight byte is read once per call, so the loads
+// are marked non-temporal and the stream does not displace the activation
+// data in L2.
+typedef unsigned int nt_u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int nt_u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ldw(const uint4* p) {
+    const nt_u4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldw(const uint2* p) {
+    const nt_u2 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u2*>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint16_t ldw(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+
 template <int DT>
 __device__ __forceinline__ void load_chunk(const WView& w, uint32_t row, uint32_t c, Chunk& ch) {
     if (DT == XNQ_Q8_0) {
         const uint32_t o = row * w.q_row + c * 32;
-        ch.q = *reinterpret_cast<const uint4*>(w.q + o);
-        ch.x = *reinterpret_cast<const uint4*>(w.q + o + 16);
-        ch.dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2)));
+        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + o));
+        ch.x = ldw(reinterpret_cast<const uint4*>(w.q + o + 16));
+        ch.dw = f16_bits_to_f32(ldw(reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2))));
     } else if (DT == XNQ_Q4_0) {
-        ch.q = *reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16));
-        ch.dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2)));
+        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
+        ch.dw = f16_bits_to_f32(ldw(reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2))));
     } else if (DT == XNQ_Q4K) {
-        ch.q = *reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16));
-        ch.x = *reinterpret_cast<const uint4*>(w.s + (row * w.s_row + (c >> 3) * 16));
+        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
+        ch.x = ldw(reinterpret_cast<const uint4*>(w.s + (row * w.s_row + (c >> 3) * 16)));
     } else {  // Q6K
         const uint32_t sb = c >> 3, j = c & 7;
-        ch.q = *reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16));
-        const uint2 h = *reinterpret_cast<const uint2*>(w.h + (row * w.h_row + c * 8));
+        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
+        const uint2 h = ldw(reinterpret_cast<const uint2*>(w.h + (row * w.h_row + c * 8)));
         ch.x.x = h.x;
         ch.x.y = h.y;
-        ch.x.z = *reinterpret_cast<const uint16_t*>(w.s + (row * w.s_row + sb * 16 + 2 * j));
-        ch.dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + sb * 2)));
+        ch.x.z = ldw(reinterpret_cast<const uint16_t*>(w.s + (row * w.s_row + sb * 16 + 2 * j)));
+        ch.dw = f16_bits_to_f32(ldw(reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + sb * 2))));
     }
 }
 
