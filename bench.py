@@ -43,8 +43,9 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=512)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy"], default="all",
-                   help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters)")
+    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "sweep"], default="all",
+                   help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters); "
+                        "'sweep' times every configured shape (matvec sweep, FFN, prefill, decode step)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one instead of replaying a HIP graph (for counter runs)")
     return p.parse_args()
@@ -107,6 +108,150 @@ def time_graph(g, stream, reps: int = 5) -> float:
     return float(np.median(times))
 
 
+WEIGHT_BYTES = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}  # dtype: (block elems, block bytes)
+
+
+def qbytes(dt: int, n: int, k: int) -> int:
+    be, bb = WEIGHT_BYTES[dt]
+    return n * (k // be) * bb
+
+
+def sweep(args, dev, stream, gen) -> dict:
+    """Every configured shape: the Q8_0 matvec, the Q4_0 FFN block with its
+    SiLU gate, the Q4_K (and Q6_K / Q4_0) matvec sweep over M = 1, 2, 4, 8,
+    the int8-MFMA prefill at M = 64 .. 2048, and all QMatMuls of one decode
+    step of the 32-layer model (batch 1 and 16).  Rates use the algorithmic
+    bytes of weights + f32 activations + f32 outputs; prefill uses 2*M*N*K."""
+    import math
+
+    import torch
+
+    from xn_amd import GgmlDType, QTensor
+    from xn_amd.quantized import lhs_workspace, matmul_preq, quantize_lhs
+
+    def make(dt, n, k):
+        w = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * 0.02
+        q = QTensor.quantize_f32(w, (n, k), GgmlDType(dt))
+        del w
+        return q
+
+    def copies_for(nbytes):
+        return max(2, min(16, math.ceil(600e6 / nbytes)))
+
+    def timed(fn, steps):
+        with torch.cuda.stream(stream):
+            for i in range(3):
+                fn(i)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            g = capture(fn, steps, stream, args.eager)
+        ms = time_graph(g, stream) / steps
+        del g
+        return ms
+
+    rows = []
+    steps = 50
+
+    def matvec_row(name, dt, k, n, ms_list):
+        wb = qbytes(dt, n, k)
+        ws = [make(dt, n, k) for _ in range(copies_for(wb))]
+        for m in ms_list:
+            x = torch.randn((m, k), generator=gen, device=dev)
+            y = torch.empty((m, n), device=dev)
+            a = lhs_workspace(GgmlDType(dt), m, k, dev)
+            quantize_lhs(GgmlDType(dt), x, a, m, k)
+            ms_step = timed(lambda i: ws[i % len(ws)].matmul_t((m, k, n), x, y), steps)
+            ms_kern = timed(lambda i: matmul_preq(ws[i % len(ws)], m, a, y), steps)
+            algo = wb + m * k * 4 + m * n * 4
+            rows.append({"config": name, "dtype": GgmlDType(dt).name, "k": k, "n": n, "m": m,
+                         "weight_copies": len(ws), "us_step": round(ms_step * 1e3, 2),
+                         "us_kernel": round(ms_kern * 1e3, 2),
+                         "gbs_step": round(algo / (ms_step * 1e-3) / 1e9, 1),
+                         "gbs_kernel": round(algo / (ms_kern * 1e-3) / 1e9, 1),
+                         "frac_hbm_kernel": round(algo / (ms_kern * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del ws
+
+    # config 1: Q8_0 4096 -> 4096
+    matvec_row("1 q8_0 matvec", 8, 4096, 4096, [1])
+    # config 3: Q4_K sweep
+    for k, n in [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 28672)]:
+        matvec_row("3 q4k sweep", 12, k, n, [1, 2, 4, 8])
+    # the other decode dtypes at the FFN shapes
+    matvec_row("5 q6k ffn down", 14, 14336, 4096, [1, 4])
+    matvec_row("2 q4_0 gate/up", 2, 4096, 14336, [1])
+    matvec_row("2 q4_0 down", 2, 14336, 4096, [1])
+
+    # config 2: Q4_0 FFN block, h = silu(x Wg^T) * (x Wu^T), y = h Wd^T
+    k, f = 4096, 14336
+    sets = [(make(2, f, k), make(2, f, k), make(2, k, f)) for _ in range(4)]
+    x = torch.randn((1, k), generator=gen, device=dev)
+    g_ = torch.empty((1, f), device=dev)
+    u_ = torch.empty((1, f), device=dev)
+    h_ = torch.empty((1, f), device=dev)
+    y_ = torch.empty((1, k), device=dev)
+
+    def ffn(i):
+        wg, wu, wd = sets[i % len(sets)]
+        wg.matmul_t((1, k, f), x, g_)
+        wu.matmul_t((1, k, f), x, u_)
+        torch.mul(torch.nn.functional.silu(g_), u_, out=h_)
+        wd.matmul_t((1, f, k), h_, y_)
+
+    ms = timed(ffn, steps)
+    algo = 3 * qbytes(2, f, k) + (2 * k + 3 * f) * 4 + f * 4
+    rows.append({"config": "2 q4_0 ffn block (silu gate, torch elementwise)", "m": 1, "us_step": round(ms * 1e3, 2),
+                 "gbs_step": round(algo / (ms * 1e-3) / 1e9, 1)})
+    print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    del sets
+
+    # config 4: prefill on int8 MFMA
+    k, n = 4096, 14336
+    for dt in (12, 14):
+        ws = [make(dt, n, k) for _ in range(copies_for(qbytes(dt, n, k)))]
+        for m in (64, 256, 512, 2048):
+            x = torch.randn((m, k), generator=gen, device=dev)
+            y = torch.empty((m, n), device=dev)
+            a = lhs_workspace(GgmlDType(dt), m, k, dev)
+            quantize_lhs(GgmlDType(dt), x, a, m, k)
+            ps = 10 if m >= 2048 else 20
+            ms_step = timed(lambda i: ws[i % len(ws)].matmul_t((m, k, n), x, y), ps)
+            ms_kern = timed(lambda i: matmul_preq(ws[i % len(ws)], m, a, y), ps)
+            ops = 2.0 * m * n * k
+            rows.append({"config": "4 prefill", "dtype": GgmlDType(dt).name, "k": k, "n": n, "m": m,
+                         "us_step": round(ms_step * 1e3, 1), "us_kernel": round(ms_kern * 1e3, 1),
+                         "tops_step": round(ops / (ms_step * 1e-3) / 1e12, 1),
+                         "tops_kernel": round(ops / (ms_kern * 1e-3) / 1e12, 1),
+                         "frac_int8_peak_kernel": round(ops / (ms_kern * 1e-3) / 1e12 / INT8_PEAK_TOPS, 3)})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del ws
+
+    # config 5: every QMatMul of one decode step (random weights; attention itself is out of scope)
+    d, kv, ff, vocab, layers = 4096, 1024, 14336, 128256, 32
+    mats = []
+    for _ in range(layers):
+        mats += [(make(12, d, d), d, d), (make(12, kv, d), d, kv), (make(12, kv, d), d, kv),
+                 (make(12, d, d), d, d), (make(12, ff, d), d, ff), (make(12, ff, d), d, ff),
+                 (make(14, d, ff), ff, d)]
+    mats.append((make(14, vocab, d), d, vocab))
+    wtotal = sum(qbytes(12 if q.dtype() == GgmlDType.Q4K else 14, n, kk) for q, kk, n in mats)
+    for b in (1, 16):
+        xs = {kk: torch.randn((b, kk), generator=gen, device=dev) for kk in (d, ff)}
+        ys = {n: torch.empty((b, n), device=dev) for n in (d, kv, ff, vocab)}
+
+        def step(i):
+            for q, kk, n in mats:
+                q.matmul_t((b, kk, n), xs[kk], ys[n])
+
+        ms = timed(step, 3)
+        rows.append({"config": "5 decode step (225 QMatMuls)", "batch": b, "weight_bytes": wtotal,
+                     "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    del mats
+    return {"metric": "per-config sweep", "rows": rows}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -151,6 +296,10 @@ def main():
         print(json.dumps({"metric": "device copy GB/s (read + write)", "bytes_read": nbytes,
                           "bytes_written": nbytes, "ms_per_copy": round(ms, 5),
                           "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}), flush=True)
+        return
+
+    if args.only == "sweep":
+        print(json.dumps(sweep(args, dev, stream, gen)), flush=True)
         return
 
     # ---------------- weights: rotated copies, quantized on the device

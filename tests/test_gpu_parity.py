@@ -140,15 +140,16 @@ def test_block_ints_bit_exact(orc, dev, dt):
 # ---------------------------------------------------------------- matmul
 @pytest.mark.parametrize("dt", WEIGHT_DTYPES)
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 17])
-def test_matmul_small(orc, dev, dt, m):
+@pytest.mark.parametrize("entry", ["matmul_t", "matmul_t_abi"])
+def test_matmul_small(orc, dev, dt, m, entry):
     rng = np.random.default_rng(6000 + 31 * dt + m)
     n, k = 300, 2048
     blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
     qt = upload(blocks, n, k, dt, dev)
     dst = torch.empty((m, n), dtype=torch.float32, device=dev)
-    qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
-    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m}")
+    getattr(qt, entry)((m, k, n), torch.from_numpy(x).to(dev), dst)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} {entry}")
 
 
 @pytest.mark.parametrize("dt,k,n", [

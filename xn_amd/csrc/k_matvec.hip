@@ -69,16 +69,16 @@ hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hip
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_matvec_fused(const WView& w, const float* x, float* y, hipStream_t s) {
+hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s) {
     AView a{};
     a.k = w.k;
-    a.m = 1;
+    a.m = (uint32_t)m;
     a.A = act_img(w.k, w.dtype == XNQ_Q4K || w.dtype == XNQ_Q6K);
     switch (w.dtype) {
-    case XNQ_Q8_0: return launch_matvec_q8_0(w, a, x, 1, y, s, true);
-    case XNQ_Q4_0: return launch_matvec_q4_0(w, a, x, 1, y, s, true);
-    case XNQ_Q4K: return launch_matvec_q4k(w, a, x, 1, y, s, true);
-    case XNQ_Q6K: return launch_matvec_q6k(w, a, x, 1, y, s, true);
+    case XNQ_Q8_0: return launch_matvec_q8_0(w, a, x, m, y, s, true);
+    case XNQ_Q4_0: return launch_matvec_q4_0(w, a, x, m, y, s, true);
+    case XNQ_Q4K: return launch_matvec_q4k(w, a, x, m, y, s, true);
+    case XNQ_Q6K: return launch_matvec_q6k(w, a, x, m, y, s, true);
     }
     return hipErrorInvalidValue;
 }

@@ -84,7 +84,7 @@ template <int DT, int MB, int kNW>
 __device__ void quantize_into_lds(const float* __restrict__ x, uint32_t k, uint32_t m0,
                                   uint32_t mcount, uint8_t* lds) {
     constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
-    constexpr int kBatch = 2;
+    constexpr int kBatch = MB < 2 ? 2 : MB;  // x loads in flight per wavefront before the first reduction
     const ActImg A = act_img(k, kq);
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -411,8 +411,9 @@ inline int pick_rows(uint32_t n, int cpl) {
     return 1;
 }
 
-// y[m x n] for all m rows: FUSED quantizes from f32 `x` (m == 1 only), else
-// reads the Q8 workspace `a`.
+// y[m x n] for all m rows, in launches of up to 8 rows: `fused` quantizes
+// each launch's rows from f32 `x` in LDS, else the kernels read the Q8
+// workspace `a`.
 template <int DT>
 hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m, float* y,
                         hipStream_t s, bool fused) {
@@ -421,17 +422,20 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
     while (gmax > 1 && lds_bytes(gmax, w.k, kq) > kMaxLds) gmax >>= 1;
     if (lds_bytes(gmax, w.k, kq) > kMaxLds) return hipErrorInvalidConfiguration;
     const int cpl = pick_cpl(w.k / 32);
-    if (fused) {
-        if (m != 1) return hipErrorInvalidValue;
-        return launch_cpl<DT, 1, true>(pick_rows(w.n, cpl), cpl, w, a, x, 0, 1, y, s);
-    }
     for (size_t m0 = 0; m0 < m; m0 += gmax) {
         const uint32_t mc = (uint32_t)((m - m0) < (size_t)gmax ? (m - m0) : (size_t)gmax);
         hipError_t e;
-        if (mc == 1) e = launch_cpl<DT, 1, false>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
-        else if (mc == 2) e = launch_cpl<DT, 2, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
-        else if (mc <= 4) e = launch_cpl<DT, 4, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
-        else e = launch_cpl<DT, 8, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        if (fused) {
+            if (mc == 1) e = launch_cpl<DT, 1, true>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc == 2) e = launch_cpl<DT, 2, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc <= 4) e = launch_cpl<DT, 4, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else e = launch_cpl<DT, 8, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        } else {
+            if (mc == 1) e = launch_cpl<DT, 1, false>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc == 2) e = launch_cpl<DT, 2, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc <= 4) e = launch_cpl<DT, 4, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else e = launch_cpl<DT, 8, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -5,6 +5,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -336,6 +337,17 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
     return XNQ_OK;
 }
 
+// Automatic route: the int8-MFMA kernel once m is large enough for its
+// 256-row tiles to pay off, the matvec kernels (up to 8 rows per launch) below
+// that.  XNQ_MFMA_MIN_ROWS overrides the crossover for tuning.
+static bool use_mfma(uint32_t dtype, size_t m, size_t n, size_t k) {
+    static const size_t min_rows = [] {
+        const char* e = getenv("XNQ_MFMA_MIN_ROWS");
+        return e ? (size_t)strtoull(e, nullptr, 10) : (size_t)9;
+    }();
+    return m >= min_rows && mfma_supported(dtype, m, n, k);
+}
+
 xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
                                    const void* workspace_dev, float* dst_dev, void* stream) {
     xnq_status st = check_mkn(qt, m, k, n);
@@ -348,8 +360,7 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     const AView a = make_aview(act_layout(qt->L.dtype, m, k), workspace_dev);
     const int route = g_route.load();
     hipError_t e;
-    const bool use_mfma = route == 2 || (route == 0 && m > 8 && mfma_supported(qt->L.dtype, m, n, k));
-    if (use_mfma) {
+    if (route == 2 || (route == 0 && use_mfma(qt->L.dtype, m, n, k))) {
         if (!mfma_supported(qt->L.dtype, m, n, k))
             return fail(XNQ_ERR_UNSUPPORTED, "no MFMA kernel for this dtype/shape");
         e = launch_mfma(w, a, m, dst_dev, (hipStream_t)stream);
@@ -374,10 +385,11 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
     const int route = g_route.load();
-    if (m == 1 && route != 2) {
-        // Decode: one kernel quantizes the row in LDS and streams the weight.
+    if (route == 1 || (route == 0 && !use_mfma(qt->L.dtype, m, n, k))) {
+        // Decode: each launch quantizes its (up to 8) rows in LDS and streams
+        // the weight; no workspace.
         const WView w = make_wview(qt->L, qt->buf);
-        hipError_t e = launch_matvec_fused(w, lhs_dev, dst_dev, s);
+        hipError_t e = launch_matvec_fused(w, lhs_dev, m, dst_dev, s);
         if (e == hipErrorInvalidConfiguration)
             return fail(XNQ_ERR_INVALID, "k = %zu is too large for the matvec kernel's LDS", k);
         if (e != hipSuccess) return hip_fail(e, "matvec kernel");

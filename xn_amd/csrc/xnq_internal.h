@@ -145,7 +145,7 @@ hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float*
 // k_matvec.hip
 hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hipStream_t s);
 // m == 1: quantizes the f32 row inside the kernel (no workspace).
-hipError_t launch_matvec_fused(const WView& w, const float* x, float* y, hipStream_t s);
+hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s);
 hipError_t launch_block_ints(const WView& w, const AView& a, size_t m,
                              int32_t* out, hipStream_t s);
 // k_mfma.hip

@@ -241,8 +241,7 @@ class QTensor:
                                                _stream(self.device)))
         return host.tobytes()
 
-    def matmul_t(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
-        """dst[m, n] = quantize(lhs[m, k]) . W^T (mod.rs:334-339, k_quants.rs:1996-2011)."""
+    def _check_mm(self, mkn, lhs: torch.Tensor, dst: torch.Tensor) -> Tuple[int, int, int]:
         m, k, n = (int(v) for v in mkn)
         if m * k != lhs.numel():
             raise XnqError(1, f"unexpected lhs length {lhs.numel()} {(m, k, n)}")
@@ -251,6 +250,30 @@ class QTensor:
         for t, name in ((lhs, "lhs"), (dst, "dst")):
             if t.device != self.device or t.dtype != torch.float32 or not t.is_contiguous():
                 raise XnqError(1, f"{name} must be a contiguous float32 tensor on {self.device}")
+        return m, k, n
+
+    def matmul_t(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
+        """dst[m, n] = quantize(lhs[m, k]) . W^T (mod.rs:334-339, k_quants.rs:1996-2011).
+
+        The quantized activation goes to a workspace from torch's caching
+        allocator (graph-capture safe, no per-call device allocation), then
+        the library's quantize_lhs and matmul_preq run on the current stream:
+        quantize_lhs + T::matmul, as k_quants::matmul does."""
+        m, k, n = self._check_mm(mkn, lhs, dst)
+        if m == 0 or n == 0:
+            return
+        dt = self.dtype()
+        ws = lhs_workspace(dt, m, k, self.device)
+        L = _lib.load()
+        st = _stream(self.device)
+        check(L.xnq_quantize_lhs(int(dt), m, k, _ptr(lhs), _ptr(ws), st))
+        check(L.xnq_qtensor_matmul_preq(self.storage.handle, m, k, n, _ptr(ws), _ptr(dst), st))
+
+    def matmul_t_abi(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
+        """The same product through the single C entry point xnq_qtensor_matmul_t
+        (what a foreign caller binds): m <= 8 quantizes inside the matvec
+        kernels, larger m uses a stream-ordered workspace."""
+        m, k, n = self._check_mm(mkn, lhs, dst)
         check(_lib.load().xnq_qtensor_matmul_t(self.storage.handle, m, k, n, _ptr(lhs), _ptr(dst),
                                                _stream(self.device)))
 
