@@ -158,7 +158,7 @@ def sweep(args, dev, stream, gen) -> dict:
         for m in ms_list:
             x = torch.randn((m, k), generator=gen, device=dev)
             y = torch.empty((m, n), device=dev)
-            a = lhs_workspace(GgmlDType(dt), m, k, dev)
+            a = ws[0].workspace(m)
             quantize_lhs(GgmlDType(dt), x, a, m, k)
             ms_step = timed(lambda i: ws[i % len(ws)].matmul_t((m, k, n), x, y), steps)
             ms_kern = timed(lambda i: matmul_preq(ws[i % len(ws)], m, a, y), steps)
@@ -212,7 +212,7 @@ def sweep(args, dev, stream, gen) -> dict:
         for m in (64, 256, 512, 2048):
             x = torch.randn((m, k), generator=gen, device=dev)
             y = torch.empty((m, n), device=dev)
-            a = lhs_workspace(GgmlDType(dt), m, k, dev)
+            a = ws[0].workspace(m)
             quantize_lhs(GgmlDType(dt), x, a, m, k)
             ps = 10 if m >= 2048 else 20
             ms_step = timed(lambda i: ws[i % len(ws)].matmul_t((m, k, n), x, y), ps)
@@ -315,7 +315,7 @@ def main():
     if args.only in ("all", "matvec"):
         x = torch.randn((1, K_DIM), generator=gen, device=dev, dtype=torch.float32)
         y = torch.empty((1, N_DIM), device=dev, dtype=torch.float32)
-        ws = lhs_workspace(GgmlDType.Q4K, 1, K_DIM, dev)
+        ws = copies[0].workspace(1)
 
         def step(i):
             copies[i % len(copies)].matmul_t((1, K_DIM, N_DIM), x, y)
@@ -362,7 +362,7 @@ def main():
         m = args.prefill_m
         xp = torch.randn((m, K_DIM), generator=gen, device=dev, dtype=torch.float32)
         yp = torch.empty((m, N_DIM), device=dev, dtype=torch.float32)
-        wsp = lhs_workspace(GgmlDType.Q4K, m, K_DIM, dev)
+        wsp = copies[0].workspace(m)
         psteps = max(5, min(50, args.steps // 4))
 
         def pstep(i):

@@ -103,14 +103,20 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
                                 const float* lhs_dev, float* dst_dev, void* stream);
 
 /* The two halves of matmul_t, for callers that keep the quantized
- * activation around (k_quants.rs:2014-2026 quantize_lhs, then T::matmul).
- * The activation workspace layout is private to the library; size it with
- * xnq_lhs_workspace_size. */
+ * activation around or manage the scratch memory themselves
+ * (k_quants.rs:2014-2026 quantize_lhs, then T::matmul).  The workspace
+ * layout is private to the library.  xnq_lhs_workspace_size gives the bytes
+ * quantize_lhs writes (the quantized activation image);
+ * xnq_qtensor_workspace_size adds the scratch matmul_preq may use on this
+ * weight (split-K partial sums of the MFMA route).  matmul_preq is told the
+ * workspace's size and uses no scratch it does not fit. */
 size_t xnq_lhs_workspace_size(uint32_t weight_dtype, size_t m, size_t k);
+size_t xnq_qtensor_workspace_size(const xnq_qtensor* qt, size_t m);
 xnq_status xnq_quantize_lhs(uint32_t weight_dtype, size_t m, size_t k, const float* lhs_dev,
                             void* workspace_dev, void* stream);
 xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
-                                   const void* workspace_dev, float* dst_dev, void* stream);
+                                   const void* workspace_dev, size_t workspace_bytes, float* dst_dev,
+                                   void* stream);
 
 /* Force a route for matmul_preq (testing and benchmarking): 0 = automatic,
  * 1 = matvec kernel, 2 = MFMA kernel.  Process wide. */

@@ -176,16 +176,24 @@ def test_matmul_config_shapes(orc, dev, dt, k, n, m):
 
 @pytest.mark.parametrize("dt", [Q4K, Q6K])
 @pytest.mark.parametrize("m,n,k", [(64, 512, 4096), (130, 512, 4096), (300, 200, 768), (9, 129, 256),
-                                   (257, 384, 1280)])
+                                   (257, 384, 1280), (16, 512, 7168), (24, 1000, 4096)])
 def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
-    """Prefill route (m > 8): ragged m and n against the tile sizes, 1-5 super-blocks."""
+    """The int8-MFMA route (forced): ragged m and n against the 256 x 128
+    tiles, 1-28 super-blocks, and grids small enough to be split along K
+    (partial sums added in a second kernel)."""
+    from xn_amd.quantized import set_route
+
     rng = np.random.default_rng(8000 + dt + m + n + k)
     blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
     qt = upload(blocks, n, k, dt, dev)
     dst = torch.empty((m, n), dtype=torch.float32, device=dev)
-    qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
-    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m}")
+    set_route(2)
+    try:
+        qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
+    finally:
+        set_route(0)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} n={n} k={k}")
 
 
 def test_qlinear_vs_linear(dev):

@@ -163,7 +163,8 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_t m, float* __restrict__ y) {
+__global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_t m, uint32_t sb_per_split,
+                                                       float* __restrict__ y, size_t split_stride) {
     using L = Lay<DT>;
     constexpr bool kQ4K = L::kQ4K;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -171,7 +172,11 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave >> 1, wn = wave & 1;  // 4 x 2 wavefronts, 64 x 64 each
     const uint32_t m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-    const uint32_t K = w.k, nsb = K / 256;
+    // split-K: this workgroup's super-blocks sb0 .. sb0 + nsb - 1; with more
+    // than one split each writes its own partial output, summed afterwards
+    const uint32_t sb0 = blockIdx.z * sb_per_split;
+    const uint32_t K = w.k, nsb = min(sb_per_split, K / 256 - sb0);
+    y += blockIdx.z * split_stride;
     const ActImg& A = a.A;
     const uint32_t lbase = (uint32_t)(uintptr_t)lds;  // low half of the flat address = LDS offset
     const uint32_t lrow = lane & 31, lgrp = lane >> 5;
@@ -182,6 +187,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
     const uint32_t row_max = m - 1 - m0, col_max = w.n - 1 - n0;
     auto a_row = [&](uint32_t r) { return min(r, row_max) * A.row_bytes; };  // byte offset of tile row r
     const uint8_t* a_img = a.img + (size_t)m0 * A.row_bytes;
+    const uint8_t* a_q = a_img + sb0 * 128;  // quants: 8 chunks of 16 bytes per super-block and half
     auto epi_base = [&](uint32_t sb) -> uint8_t* { return lds + L::kOffEpi + (sb & 1) * L::kEpi; };
 
     v16f accf[kTM][kTN];
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         } else {
             // d rows are padded to 4 bytes: the dword holds super-blocks 2*(sb/2), +1
             const uint32_t dd = reinterpret_cast<const uint32_t*>(epi + L::kEB)[nl];
-            dw = f16_bits_to_f32((sb & 1) ? (dd >> 16) : (dd & 0xffffu));
+            dw = f16_bits_to_f32(((sb0 + sb) & 1) ? (dd >> 16) : (dd & 0xffffu));
         }
         const uint32_t rl = wm * 64 + i * 32;
 #pragma unroll
@@ -237,9 +243,9 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         const uint32_t bc = gw >> 1, cw = gw & 1;      // group 0: chunk and 64-column half
         const uint32_t col = cw * 64 + lane;           // group 0: this lane's weight column
         const uint32_t q_lane = min(col, col_max) * w.q_row;
-        const uint8_t* wq = w.q + (size_t)n0 * w.q_row;
-        const uint8_t* wh = w.h + (size_t)n0 * w.h_row;
-        const uint8_t* ws = w.s + (size_t)n0 * w.s_row;
+        const uint8_t* wq = w.q + (size_t)n0 * w.q_row + sb0 * 128;
+        const uint8_t* wh = w.h + (size_t)n0 * w.h_row + sb0 * 64;
+        const uint8_t* ws = w.s + (size_t)n0 * w.s_row + sb0 * 16;
         const uint8_t* wd = w.d + (size_t)n0 * w.d_row;
         const uint32_t nstage = 4 * nsb;
 
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
             if (p < 2) {
                 // activation piece t = 2*wave + p: (ks, h, 64-row block)
                 const uint32_t t = 2 * wave + p, ks = t >> 3, h = (t >> 2) & 1, rb = t & 3;
-                dma16(a_img + h * (K / 2) + ks * 16 + st * 32, a_row(rb * 64 + lane),
+                dma16(a_q + h * (K / 2) + ks * 16 + st * 32, a_row(rb * 64 + lane),
                       lbase + L::kOffA + slot * L::kASlot + ((ks * 2 + h) * kBM + rb * 64) * 16);
                 return;
             }
@@ -260,12 +266,12 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                 if (!kQ4K && p == 3) dma16(wh + st * 16, q_lane >> 1, raw + L::kQSlot);  // qh of chunks 2st, 2st+1
                 if (p == kBase) dma16(ws + sb * 16, q_lane >> 3, epi + L::kEHdr + cw * 64 * 16);
                 if (!kQ4K && p == kBase + 1)
-                    dma4(wd + (sb & ~1u) * 2, min(col, col_max) * w.d_row, epi + L::kEB + cw * 64 * 4);
+                    dma4(wd + ((sb0 + sb) & ~1u) * 2, min(col, col_max) * w.d_row, epi + L::kEB + cw * 64 * 4);
             } else {
-                if (p == kBase) dma4(a_img + A.d_off + sb * 4, a_row(64 * gw + lane), epi + L::kEDa + 64 * gw * 4);
+                if (p == kBase) dma4(a_img + A.d_off + (sb0 + sb) * 4, a_row(64 * gw + lane), epi + L::kEDa + 64 * gw * 4);
                 if (kQ4K && p > kBase) {
                     const uint32_t i = p - kBase - 1;  // rows 64*gw + 32*i + lane/2
-                    dma16(a_img + A.s_off + sb * 32, a_row(64 * gw + 32 * i + (lane >> 1)) + (lane & 1) * 16,
+                    dma16(a_img + A.s_off + (sb0 + sb) * 32, a_row(64 * gw + 32 * i + (lane >> 1)) + (lane & 1) * 16,
                           epi + L::kESum + (64 * gw + 32 * i) * 32);
                 }
             }
@@ -481,8 +487,33 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         }
 }
 
+// y = sum of the split-K partial outputs, in split order (deterministic).
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part, size_t count,
+                                                         uint32_t splits, float* __restrict__ y) {
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (count % 4 == 0) {
+        if (i4 * 4 >= count) return;
+        float4 acc = reinterpret_cast<const float4*>(part)[i4];
+        for (uint32_t z = 1; z < splits; z++) {
+            const float4 v = reinterpret_cast<const float4*>(part + z * count)[i4];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        reinterpret_cast<float4*>(y)[i4] = acc;
+        return;
+    }
+    for (size_t i = i4 * 4; i < i4 * 4 + 4 && i < count; i++) {
+        float acc = part[i];
+        for (uint32_t z = 1; z < splits; z++) acc += part[z * count + i];
+        y[i] = acc;
+    }
+}
+
 template <int DT>
-hipError_t launch_dt(const WView& w, const AView& a, size_t m, float* y, hipStream_t s) {
+hipError_t launch_dt(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
+                     hipStream_t s) {
     static bool attr = false;
     if (!attr) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_kernel<DT>),
@@ -490,8 +521,18 @@ hipError_t launch_dt(const WView& w, const AView& a, size_t m, float* y, hipStre
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid((w.n + kBN - 1) / kBN, (unsigned)((m + kBM - 1) / kBM));
-    hipLaunchKernelGGL(qmm_kernel<DT>, grid, dim3(kThreads), Lay<DT>::kLds, s, w, a, (uint32_t)m, y);
+    const uint32_t nsb = w.k / 256;
+    const uint32_t per = (nsb + splits - 1) / splits;
+    splits = (nsb + per - 1) / per;  // every split non-empty
+    const dim3 grid((w.n + kBN - 1) / kBN, (unsigned)((m + kBM - 1) / kBM), splits);
+    float* out = splits > 1 ? partial : y;
+    hipLaunchKernelGGL(qmm_kernel<DT>, grid, dim3(kThreads), Lay<DT>::kLds, s, w, a, (uint32_t)m, per, out,
+                       splits > 1 ? m * (size_t)w.n : (size_t)0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    const size_t count = m * (size_t)w.n;
+    const unsigned blocks = (unsigned)((count / 4 + 255) / 256 + 1);
+    hipLaunchKernelGGL(sum_splits_kernel, dim3(blocks), dim3(256), 0, s, partial, count, splits, y);
     return hipGetLastError();
 }
 
@@ -503,10 +544,22 @@ bool mfma_supported(uint32_t dtype, size_t m, size_t n, size_t k) {
     return (dtype == XNQ_Q4K || dtype == XNQ_Q6K) && k % 256 == 0;
 }
 
-hipError_t launch_mfma(const WView& w, const AView& a, size_t m, float* y, hipStream_t s) {
+uint32_t mfma_splits(size_t m, size_t n, size_t k) {
+    // Split K while whole splits of the grid still fit on the 256 CUs at
+    // once (one workgroup per CU), each split at least two super-blocks long.
+    const size_t tiles = ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM);
+    const size_t nsb = k / 256;
+    size_t splits = 256 / tiles;
+    if (splits > nsb / 2) splits = nsb / 2;
+    return splits < 1 ? 1u : (uint32_t)splits;
+}
+
+hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
+                       hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    if (w.dtype == XNQ_Q4K) return launch_dt<XNQ_Q4K>(w, a, m, y, s);
-    if (w.dtype == XNQ_Q6K) return launch_dt<XNQ_Q6K>(w, a, m, y, s);
+    if (splits > 1 && !partial) splits = 1;
+    if (w.dtype == XNQ_Q4K) return launch_dt<XNQ_Q4K>(w, a, m, splits, y, partial, s);
+    if (w.dtype == XNQ_Q6K) return launch_dt<XNQ_Q6K>(w, a, m, splits, y, partial, s);
     return hipErrorNotSupported;
 }
 

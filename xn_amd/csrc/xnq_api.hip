@@ -196,7 +196,7 @@ extern "C" {
 
 const char* xnq_last_error(void) { return g_err.c_str(); }
 
-int xnq_abi_version(void) { return 1; }
+int xnq_abi_version(void) { return 2; }
 
 size_t xnq_type_size(uint32_t dtype) { return type_size(dtype); }
 size_t xnq_block_size(uint32_t dtype) { return block_size(dtype); }
@@ -299,6 +299,22 @@ size_t xnq_lhs_workspace_size(uint32_t weight_dtype, size_t m, size_t k) {
     return act_layout(weight_dtype, m, k).bytes;
 }
 
+// Split-K partial sums of the MFMA route sit after the activation image.
+static size_t partial_offset(uint32_t dtype, size_t m, size_t k) {
+    return (act_layout(dtype, m, k).bytes + kAlign - 1) / kAlign * kAlign;
+}
+
+size_t xnq_qtensor_workspace_size(const xnq_qtensor* qt, size_t m) {
+    if (!qt) return 0;
+    const size_t k = qt->L.k, n = qt->L.n;
+    size_t bytes = act_layout(qt->L.dtype, m, k).bytes;
+    if (mfma_supported(qt->L.dtype, m, n, k)) {
+        const uint32_t splits = mfma_splits(m, n, k);
+        if (splits > 1) bytes = partial_offset(qt->L.dtype, m, k) + (size_t)splits * m * n * sizeof(float);
+    }
+    return bytes;
+}
+
 static xnq_status check_lhs(uint32_t weight_dtype, size_t k) {
     const uint32_t vt = vec_dot_type(weight_dtype);
     const size_t bs = block_size(vt);
@@ -337,19 +353,22 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
     return XNQ_OK;
 }
 
-// Automatic route: the int8-MFMA kernel once m is large enough for its
-// 256-row tiles to pay off, the matvec kernels (up to 8 rows per launch) below
-// that.  XNQ_MFMA_MIN_ROWS overrides the crossover for tuning.
+// Automatic route: the int8-MFMA kernel once m is large enough for it to
+// beat the matvec kernels (which take up to 8 rows per launch).  Measured
+// crossover on MI355X: m >= 9 when k >= 8192 (the matvec's per-row work is
+// long), m >= 20 otherwise.  XNQ_MFMA_MIN_ROWS overrides it for tuning.
 static bool use_mfma(uint32_t dtype, size_t m, size_t n, size_t k) {
-    static const size_t min_rows = [] {
+    static const size_t forced = [] {
         const char* e = getenv("XNQ_MFMA_MIN_ROWS");
-        return e ? (size_t)strtoull(e, nullptr, 10) : (size_t)9;
+        return e ? (size_t)strtoull(e, nullptr, 10) : (size_t)0;
     }();
+    const size_t min_rows = forced ? forced : (k >= 8192 ? 9 : 20);
     return m >= min_rows && mfma_supported(dtype, m, n, k);
 }
 
 xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
-                                   const void* workspace_dev, float* dst_dev, void* stream) {
+                                   const void* workspace_dev, size_t workspace_bytes, float* dst_dev,
+                                   void* stream) {
     xnq_status st = check_mkn(qt, m, k, n);
     if (st) return st;
     if (m == 0 || n == 0) return XNQ_OK;
@@ -363,7 +382,11 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     if (route == 2 || (route == 0 && use_mfma(qt->L.dtype, m, n, k))) {
         if (!mfma_supported(qt->L.dtype, m, n, k))
             return fail(XNQ_ERR_UNSUPPORTED, "no MFMA kernel for this dtype/shape");
-        e = launch_mfma(w, a, m, dst_dev, (hipStream_t)stream);
+        uint32_t splits = mfma_splits(m, n, k);
+        const size_t off = partial_offset(qt->L.dtype, m, k);
+        if (off + (size_t)splits * m * n * sizeof(float) > workspace_bytes) splits = 1;
+        float* partial = splits > 1 ? reinterpret_cast<float*>((uint8_t*)workspace_dev + off) : nullptr;
+        e = launch_mfma(w, a, m, splits, dst_dev, partial, (hipStream_t)stream);
     } else {
         e = launch_matvec(w, a, m, dst_dev, (hipStream_t)stream);
     }
@@ -395,12 +418,12 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
         if (e != hipSuccess) return hip_fail(e, "matvec kernel");
         return XNQ_OK;
     }
-    const ALayout A = act_layout(qt->L.dtype, m, k);
+    const size_t ws_bytes = xnq_qtensor_workspace_size(qt, m);
     void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, A.bytes, s);
+    hipError_t e = hipMallocAsync(&ws, ws_bytes, s);
     if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(workspace)");
     st = xnq_quantize_lhs(qt->L.dtype, m, k, lhs_dev, ws, stream);
-    if (!st) st = xnq_qtensor_matmul_preq(qt, m, k, n, ws, dst_dev, stream);
+    if (!st) st = xnq_qtensor_matmul_preq(qt, m, k, n, ws, ws_bytes, dst_dev, stream);
     (void)hipFreeAsync(ws, s);
     return st;
 }

@@ -150,7 +150,8 @@ hipError_t launch_block_ints(const WView& w, const AView& a, size_t m,
                              int32_t* out, hipStream_t s);
 // k_mfma.hip
 bool mfma_supported(uint32_t dtype, size_t m, size_t n, size_t k);
-hipError_t launch_mfma(const WView& w, const AView& a, size_t m, float* y,
+uint32_t mfma_splits(size_t m, size_t n, size_t k);
+hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                        hipStream_t s);
 
 }  // namespace xnq

@@ -263,11 +263,16 @@ class QTensor:
         if m == 0 or n == 0:
             return
         dt = self.dtype()
-        ws = lhs_workspace(dt, m, k, self.device)
+        ws = self.workspace(m)
         L = _lib.load()
         st = _stream(self.device)
         check(L.xnq_quantize_lhs(int(dt), m, k, _ptr(lhs), _ptr(ws), st))
-        check(L.xnq_qtensor_matmul_preq(self.storage.handle, m, k, n, _ptr(ws), _ptr(dst), st))
+        check(L.xnq_qtensor_matmul_preq(self.storage.handle, m, k, n, _ptr(ws), ws.numel(), _ptr(dst), st))
+
+    def workspace(self, m: int) -> torch.Tensor:
+        """Scratch for quantize_lhs + matmul_preq of m rows on this weight."""
+        nbytes = _lib.load().xnq_qtensor_workspace_size(self.storage.handle, int(m))
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
 
     def matmul_t_abi(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
         """The same product through the single C entry point xnq_qtensor_matmul_t
@@ -369,7 +374,7 @@ def quantize_lhs(dtype: GgmlDType, lhs: torch.Tensor, ws: torch.Tensor, m: int, 
 
 def matmul_preq(qt: QTensor, m: int, ws: torch.Tensor, dst: torch.Tensor) -> None:
     n, k = qt.storage.rows(), qt.storage.cols()
-    check(_lib.load().xnq_qtensor_matmul_preq(qt.storage.handle, m, k, n, _ptr(ws), _ptr(dst),
+    check(_lib.load().xnq_qtensor_matmul_preq(qt.storage.handle, m, k, n, _ptr(ws), ws.numel(), _ptr(dst),
                                               _stream(dst.device)))
 
 
