@@ -118,8 +118,9 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
                                    const void* workspace_dev, size_t workspace_bytes, float* dst_dev,
                                    void* stream);
 
-/* Force a route for matmul_preq (testing and benchmarking): 0 = automatic,
- * 1 = matvec kernel, 2 = MFMA kernel.  Process wide. */
+/* Force a route for matmul_t / matmul_preq (testing and benchmarking):
+ * 0 = automatic, 1 = matvec kernels, 2 = tiled int8-MFMA (prefill) kernel,
+ * 3 = skinny int8-MFMA kernel (m <= 64).  Process wide. */
 xnq_status xnq_set_route(int route);
 
 /* Dequantize into elem_count f32 values (QTensor::dequantize /

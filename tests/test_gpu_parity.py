@@ -196,6 +196,27 @@ def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
     assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
+@pytest.mark.parametrize("m,n,k", [(2, 300, 2048), (5, 129, 768), (8, 512, 4096), (16, 200, 1024),
+                                   (31, 384, 2304), (33, 256, 1280), (64, 130, 512)])
+def test_matmul_skinny(orc, dev, dt, m, n, k):
+    """The skinny int8-MFMA route (forced) for 2 <= m <= 64: one and two 32-row
+    tiles, ragged n against the 128-column workgroups, split-K."""
+    from xn_amd.quantized import set_route
+
+    rng = np.random.default_rng(8500 + dt + m + n + k)
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    set_route(3)
+    try:
+        qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
+    finally:
+        set_route(0)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} n={n} k={k}")
+
+
 def test_qlinear_vs_linear(dev):
     """tests/quantized_tests.rs:14-118: QLinear(Q8_0) vs f32 Linear, 64->32,
     batch 4 (and 2x3 3-D input), max error < 0.3, with and without bias."""

@@ -44,6 +44,40 @@ namespace xnq {
 
 namespace {
 
+// y = sum of the split-K partial outputs, in split order (deterministic).
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part, size_t count,
+                                                         uint32_t splits, float* __restrict__ y) {
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (count % 4 == 0) {
+        if (i4 * 4 >= count) return;
+        float4 acc = reinterpret_cast<const float4*>(part)[i4];
+        for (uint32_t z = 1; z < splits; z++) {
+            const float4 v = reinterpret_cast<const float4*>(part + z * count)[i4];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        reinterpret_cast<float4*>(y)[i4] = acc;
+        return;
+    }
+    for (size_t i = i4 * 4; i < i4 * 4 + 4 && i < count; i++) {
+        float acc = part[i];
+        for (uint32_t z = 1; z < splits; z++) acc += part[z * count + i];
+        y[i] = acc;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_sum_splits(const float* partial, size_t count, uint32_t splits, float* y, hipStream_t s) {
+    const unsigned blocks = (unsigned)((count / 4 + 255) / 256 + 1);
+    hipLaunchKernelGGL(sum_splits_kernel, dim3(blocks), dim3(256), 0, s, partial, count, splits, y);
+    return hipGetLastError();
+}
+
+namespace {
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -102,23 +136,6 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t ld
                  "v"(off), "s"(base)
                  : "memory");
 }
-// Wait until at most n of this wavefront's vector memory operations are
-// outstanding (n is wavefront-uniform; counts above 31 wait for all).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-#define XNQ_W(N)                                              \
-    case N:                                                   \
-        asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
-        break;
-        XNQ_W(1) XNQ_W(2) XNQ_W(3) XNQ_W(4) XNQ_W(5) XNQ_W(6) XNQ_W(7) XNQ_W(8)
-        XNQ_W(9) XNQ_W(10) XNQ_W(11) XNQ_W(12) XNQ_W(13) XNQ_W(14) XNQ_W(15) XNQ_W(16)
-        XNQ_W(17) XNQ_W(18) XNQ_W(19) XNQ_W(20) XNQ_W(21) XNQ_W(22) XNQ_W(23) XNQ_W(24)
-        XNQ_W(25) XNQ_W(26) XNQ_W(27) XNQ_W(28) XNQ_W(29) XNQ_W(30) XNQ_W(31)
-#undef XNQ_W
-    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    }
-}
-
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
 // bytes of d (each <= 15) times s (<= 7): every product is <= 105, so no
@@ -487,30 +504,6 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         }
 }
 
-// y = sum of the split-K partial outputs, in split order (deterministic).
-__global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part, size_t count,
-                                                         uint32_t splits, float* __restrict__ y) {
-    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (count % 4 == 0) {
-        if (i4 * 4 >= count) return;
-        float4 acc = reinterpret_cast<const float4*>(part)[i4];
-        for (uint32_t z = 1; z < splits; z++) {
-            const float4 v = reinterpret_cast<const float4*>(part + z * count)[i4];
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
-        }
-        reinterpret_cast<float4*>(y)[i4] = acc;
-        return;
-    }
-    for (size_t i = i4 * 4; i < i4 * 4 + 4 && i < count; i++) {
-        float acc = part[i];
-        for (uint32_t z = 1; z < splits; z++) acc += part[z * count + i];
-        y[i] = acc;
-    }
-}
-
 template <int DT>
 hipError_t launch_dt(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                      hipStream_t s) {
@@ -531,9 +524,7 @@ hipError_t launch_dt(const WView& w, const AView& a, size_t m, uint32_t splits, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
     const size_t count = m * (size_t)w.n;
-    const unsigned blocks = (unsigned)((count / 4 + 255) / 256 + 1);
-    hipLaunchKernelGGL(sum_splits_kernel, dim3(blocks), dim3(256), 0, s, partial, count, splits, y);
-    return hipGetLastError();
+    return launch_sum_splits(partial, count, splits, y, s);
 }
 
 }  // namespace

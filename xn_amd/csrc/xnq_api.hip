@@ -299,22 +299,6 @@ size_t xnq_lhs_workspace_size(uint32_t weight_dtype, size_t m, size_t k) {
     return act_layout(weight_dtype, m, k).bytes;
 }
 
-// Split-K partial sums of the MFMA route sit after the activation image.
-static size_t partial_offset(uint32_t dtype, size_t m, size_t k) {
-    return (act_layout(dtype, m, k).bytes + kAlign - 1) / kAlign * kAlign;
-}
-
-size_t xnq_qtensor_workspace_size(const xnq_qtensor* qt, size_t m) {
-    if (!qt) return 0;
-    const size_t k = qt->L.k, n = qt->L.n;
-    size_t bytes = act_layout(qt->L.dtype, m, k).bytes;
-    if (mfma_supported(qt->L.dtype, m, n, k)) {
-        const uint32_t splits = mfma_splits(m, n, k);
-        if (splits > 1) bytes = partial_offset(qt->L.dtype, m, k) + (size_t)splits * m * n * sizeof(float);
-    }
-    return bytes;
-}
-
 static xnq_status check_lhs(uint32_t weight_dtype, size_t k) {
     const uint32_t vt = vec_dot_type(weight_dtype);
     const size_t bs = block_size(vt);
@@ -339,7 +323,7 @@ xnq_status xnq_quantize_lhs(uint32_t weight_dtype, size_t m, size_t k, const flo
 }
 
 xnq_status xnq_set_route(int route) {
-    if (route < 0 || route > 2) return fail(XNQ_ERR_INVALID, "route must be 0, 1 or 2");
+    if (route < 0 || route > 3) return fail(XNQ_ERR_INVALID, "route must be 0, 1, 2 or 3");
     g_route.store(route);
     return XNQ_OK;
 }
@@ -353,17 +337,50 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
     return XNQ_OK;
 }
 
-// Automatic route: the int8-MFMA kernel once m is large enough for it to
-// beat the matvec kernels (which take up to 8 rows per launch).  Measured
-// crossover on MI355X: m >= 9 when k >= 8192 (the matvec's per-row work is
-// long), m >= 20 otherwise.  XNQ_MFMA_MIN_ROWS overrides it for tuning.
-static bool use_mfma(uint32_t dtype, size_t m, size_t n, size_t k) {
-    static const size_t forced = [] {
-        const char* e = getenv("XNQ_MFMA_MIN_ROWS");
-        return e ? (size_t)strtoull(e, nullptr, 10) : (size_t)0;
-    }();
-    const size_t min_rows = forced ? forced : (k >= 8192 ? 9 : 20);
-    return m >= min_rows && mfma_supported(dtype, m, n, k);
+// Automatic routes (measured on MI355X):
+//   m < 12 (m < 8 when k >= 8192)   matvec kernels (up to 8 rows per launch)
+//   m <= 64                          skinny int8-MFMA kernel for Q4K / Q6K
+//   larger m                         tiled int8-MFMA prefill kernel
+// Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MAX_ROWS and
+// XNQ_MFMA_MIN_ROWS override the crossovers for tuning.
+enum Route { kMatvec, kSkinny, kMfma };
+
+static size_t env_size(const char* name, size_t dflt) {
+    const char* e = getenv(name);
+    return e ? (size_t)strtoull(e, nullptr, 10) : dflt;
+}
+
+static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k) {
+    static const size_t skinny_min = env_size("XNQ_SKINNY_MIN_ROWS", 0);
+    static const size_t skinny_max = env_size("XNQ_SKINNY_MAX_ROWS", 64);
+    const int forced = g_route.load();
+    if (forced == 1) return kMatvec;
+    if (forced == 2) return kMfma;
+    if (forced == 3) return kSkinny;
+    const size_t skinny_lo = skinny_min ? skinny_min : (k >= 8192 ? 8 : 12);
+    if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
+    if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
+    return kMatvec;
+}
+
+// Split-K partial sums sit after the activation image in the workspace.
+static size_t partial_offset(uint32_t dtype, size_t m, size_t k) {
+    return (act_layout(dtype, m, k).bytes + kAlign - 1) / kAlign * kAlign;
+}
+
+static uint32_t route_splits(Route r, size_t m, size_t n, size_t k) {
+    if (r == kMfma) return mfma_splits(m, n, k);
+    if (r == kSkinny) return skinny_splits(m, n, k);
+    return 1;
+}
+
+size_t xnq_qtensor_workspace_size(const xnq_qtensor* qt, size_t m) {
+    if (!qt) return 0;
+    const size_t k = qt->L.k, n = qt->L.n;
+    size_t bytes = act_layout(qt->L.dtype, m, k).bytes;
+    const uint32_t splits = route_splits(pick_route(qt->L.dtype, m, n, k), m, n, k);
+    if (splits > 1) bytes = partial_offset(qt->L.dtype, m, k) + (size_t)splits * m * n * sizeof(float);
+    return bytes;
 }
 
 xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
@@ -377,16 +394,17 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     const WView w = make_wview(qt->L, qt->buf);
     const AView a = make_aview(act_layout(qt->L.dtype, m, k), workspace_dev);
-    const int route = g_route.load();
     hipError_t e;
-    if (route == 2 || (route == 0 && use_mfma(qt->L.dtype, m, n, k))) {
-        if (!mfma_supported(qt->L.dtype, m, n, k))
+    const Route r = pick_route(qt->L.dtype, m, n, k);
+    if (r == kMfma || r == kSkinny) {
+        if (r == kMfma ? !mfma_supported(qt->L.dtype, m, n, k) : !skinny_supported(qt->L.dtype, m, n, k))
             return fail(XNQ_ERR_UNSUPPORTED, "no MFMA kernel for this dtype/shape");
-        uint32_t splits = mfma_splits(m, n, k);
+        uint32_t splits = route_splits(r, m, n, k);
         const size_t off = partial_offset(qt->L.dtype, m, k);
         if (off + (size_t)splits * m * n * sizeof(float) > workspace_bytes) splits = 1;
         float* partial = splits > 1 ? reinterpret_cast<float*>((uint8_t*)workspace_dev + off) : nullptr;
-        e = launch_mfma(w, a, m, splits, dst_dev, partial, (hipStream_t)stream);
+        e = r == kMfma ? launch_mfma(w, a, m, splits, dst_dev, partial, (hipStream_t)stream)
+                       : launch_skinny(w, a, m, splits, dst_dev, partial, (hipStream_t)stream);
     } else {
         e = launch_matvec(w, a, m, dst_dev, (hipStream_t)stream);
     }
@@ -407,8 +425,8 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
-    const int route = g_route.load();
-    if (route == 1 || (route == 0 && !use_mfma(qt->L.dtype, m, n, k))) {
+    const Route r = pick_route(qt->L.dtype, m, n, k);
+    if (r == kMatvec && (m <= 8 || g_route.load() == 1)) {
         // Decode: each launch quantizes its (up to 8) rows in LDS and streams
         // the weight; no workspace.
         const WView w = make_wview(qt->L, qt->buf);

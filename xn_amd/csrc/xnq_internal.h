@@ -151,6 +151,12 @@ hipError_t launch_block_ints(const WView& w, const AView& a, size_t m,
 // k_mfma.hip
 bool mfma_supported(uint32_t dtype, size_t m, size_t n, size_t k);
 uint32_t mfma_splits(size_t m, size_t n, size_t k);
+bool skinny_supported(uint32_t dtype, size_t m, size_t n, size_t k);
+uint32_t skinny_splits(size_t m, size_t n, size_t k);
+hipError_t launch_skinny(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
+                         hipStream_t s);
+// y[i] = sum over z < splits of partial[z * count + i], in z order
+hipError_t launch_sum_splits(const float* partial, size_t count, uint32_t splits, float* y, hipStream_t s);
 hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                        hipStream_t s);
 
