@@ -5,6 +5,7 @@ include/xnq.h); this package is the host-side mirror of xn's quantized
 tensor API (QTensor / QLinear / BackendQ) over that library.
 """
 from ._lib import XnqError, load  # noqa: F401
+from . import gguf  # noqa: F401
 from .quantized import (  # noqa: F401
     DEVICE_DTYPES,
     GgmlDType,
@@ -20,5 +21,5 @@ from .quantized import (  # noqa: F401
 
 __all__ = [
     "XnqError", "load", "GgmlDType", "QTensor", "QStorage", "QLinear", "Q40Hip", "Q80Hip",
-    "Q4kHip", "Q6kHip", "DEVICE_DTYPES", "vec_dot_type",
+    "Q4kHip", "Q6kHip", "DEVICE_DTYPES", "vec_dot_type", "gguf",
 ]
