@@ -323,6 +323,9 @@ def main():
         def kernel_only(i):
             matmul_preq(copies[i % len(copies)], 1, ws, y)
 
+        def split_step(i):
+            copies[i % len(copies)].matmul_t_split((1, K_DIM, N_DIM), x, y)
+
         with torch.cuda.stream(stream):
             for i in range(args.warmup):
                 step(i)
@@ -333,9 +336,16 @@ def main():
         with torch.cuda.stream(stream):
             g_step = capture(step, args.steps, stream, args.eager)
             g_kern = capture(kernel_only, args.steps, stream, args.eager)
+            g_split = capture(split_step, args.steps, stream, args.eager)
         torch.cuda.synchronize()
         ms_step = time_graph(g_step, stream) / args.steps
         ms_kern = time_graph(g_kern, stream) / args.steps
+        ms_split = time_graph(g_split, stream) / args.steps
+        result["matvec_variants_us"] = {
+            "fused_step": round(ms_step * 1e3, 3),
+            "preq_kernel": round(ms_kern * 1e3, 3),
+            "quantize_then_preq_step": round(ms_split * 1e3, 3),
+        }
         value = algo_bytes / (ms_step * 1e-3) / 1e9
         achieved = algo_bytes / (ms_kern * 1e-3) / 1e9
         result.update({
@@ -356,7 +366,7 @@ def main():
             "algorithmic_bytes_per_launch": algo_bytes,
             "avg_launch_us": round(ms_kern * 1e3, 3),
         }
-        del g_step, g_kern
+        del g_step, g_kern, g_split
 
     if args.only in ("all", "prefill"):
         m = args.prefill_m

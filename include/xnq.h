@@ -102,6 +102,16 @@ size_t xnq_qtensor_device_bytes(const xnq_qtensor* qt);
 xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
                                 const float* lhs_dev, float* dst_dev, void* stream);
 
+/* matmul_t with caller-owned scratch (no allocation inside): workspace_dev
+ * holds at least xnq_qtensor_matmul_t_workspace_size(qt, m) bytes, which is
+ * 0 on the decode route (m <= 8 rows quantized in LDS by the matvec kernels;
+ * workspace_dev may then be NULL).  Same contract as xnq_qtensor_matmul_t
+ * (QTensor::matmul_t, mod.rs:334-339; k_quants::matmul, k_quants.rs:1996-2011). */
+size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m);
+xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                   const float* lhs_dev, void* workspace_dev, size_t workspace_bytes,
+                                   float* dst_dev, void* stream);
+
 /* The two halves of matmul_t, for callers that keep the quantized
  * activation around or manage the scratch memory themselves
  * (k_quants.rs:2014-2026 quantize_lhs, then T::matmul).  The workspace

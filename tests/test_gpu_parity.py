@@ -140,7 +140,7 @@ def test_block_ints_bit_exact(orc, dev, dt):
 # ---------------------------------------------------------------- matmul
 @pytest.mark.parametrize("dt", WEIGHT_DTYPES)
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 17])
-@pytest.mark.parametrize("entry", ["matmul_t", "matmul_t_abi"])
+@pytest.mark.parametrize("entry", ["matmul_t", "matmul_t_abi", "matmul_t_split"])
 def test_matmul_small(orc, dev, dt, m, entry):
     rng = np.random.default_rng(6000 + 31 * dt + m)
     n, k = 300, 2048

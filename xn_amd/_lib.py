@@ -36,6 +36,8 @@ SIGNATURES = {
     "xnq_qtensor_storage_size": (c_size, [c_void]),
     "xnq_qtensor_device_bytes": (c_size, [c_void]),
     "xnq_qtensor_matmul_t": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_void]),
+    "xnq_qtensor_matmul_t_workspace_size": (c_size, [c_void, c_size]),
+    "xnq_qtensor_matmul_t_ws": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void]),
     "xnq_lhs_workspace_size": (c_size, [c_u32, c_size, c_size]),
     "xnq_qtensor_workspace_size": (c_size, [c_void, c_size]),
     "xnq_quantize_lhs": (c_int, [c_u32, c_size, c_size, c_void, c_void, c_void]),

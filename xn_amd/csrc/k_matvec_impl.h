@@ -14,6 +14,7 @@
 // Integer dot products use v_dot4_i32_i8; block scales are applied in f32.
 #pragma once
 
+#include <algorithm>
 #include <cstdlib>
 #include <map>
 #include <mutex>
@@ -80,58 +81,65 @@ __device__ void stage_activations(const AView& a, uint32_t m0, uint32_t mcount, 
 
 // Quantize MB f32 rows straight into the LDS images (the same bytes as the
 // standalone quantize kernel: both go through q8k/q80 quant + store).
-template <int DT, int MB, int kNW>
-__device__ void quantize_into_lds(const float* __restrict__ x, uint32_t k, uint32_t m0,
-                                  uint32_t mcount, uint8_t* lds) {
-    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
-    constexpr int kBatch = MB < 2 ? 2 : MB;  // x loads in flight per wavefront before the first reduction
-    const ActImg A = act_img(k, kq);
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    if (kq) {
-        const uint32_t nb = k / 256, total = MB * nb;
-        for (uint32_t b0 = wave; b0 < total; b0 += kBatch * kNW) {  // uniform per wavefront
-            float4 v[kBatch];
+// Work is cut in rounds of kBatch blocks per wavefront; `load` issues one
+// round's f32 loads and `quant` turns them into LDS bytes.  The kernel loads
+// the first round before it issues any weight load: loads complete in order
+// (one vmcnt counter), so x loaded after the weights would wait for the HBM
+// weight stream.
+template <int DT, int MB, int kNW, int kBatch>
+struct XQuant {
+    static constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    float4 v[kBatch];
+    // first block of round 0 for this wavefront, and the block step between rounds
+    __device__ __forceinline__ static uint32_t first(uint32_t wave) { return kq ? wave : wave * 8; }
+    __device__ __forceinline__ static uint32_t step() { return kq ? kBatch * kNW : kBatch * kNW * 8; }
+    __device__ __forceinline__ static uint32_t total(uint32_t k) { return MB * (kq ? k / 256 : k / 32); }
+
+    __device__ __forceinline__ void load(const float* __restrict__ x, uint32_t k, uint32_t m0, uint32_t mcount,
+                                         uint32_t b0, uint32_t lane) {
 #pragma unroll
-            for (int j = 0; j < kBatch; j++) {
-                const uint32_t b = b0 + j * kNW, mb = b / nb, bb = b % nb;
-                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (b < total && mb < mcount)
-                    v[j] = reinterpret_cast<const float4*>(x + (size_t)(m0 + mb) * k + bb * 256)[lane];
-            }
-#pragma unroll
-            for (int j = 0; j < kBatch; j++) {
-                const uint32_t b = b0 + j * kNW;
-                if (b < total) {
-                    const Q8KLane r = q8k_quant_wave(v[j], lane);
-                    q8k_store(lds + (b / nb) * A.row_bytes, A, b % nb, lane, r);
-                }
-            }
-        }
-    } else {
-        const uint32_t nb = k / 32, total = MB * nb;
-        const int sub = lane & 7;
-        for (uint32_t b0 = wave * 8; b0 < total; b0 += kBatch * kNW * 8) {  // uniform per wavefront
-            float4 v[kBatch];
-#pragma unroll
-            for (int j = 0; j < kBatch; j++) {
-                const uint32_t b = b0 + j * kNW * 8 + (lane >> 3), mb = b / nb, c = b % nb;
-                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (b < total && mb < mcount)
-                    v[j] = reinterpret_cast<const float4*>(x + (size_t)(m0 + mb) * k + c * 32)[sub];
-            }
-#pragma unroll
-            for (int j = 0; j < kBatch; j++) {
-                const uint32_t bw = b0 + j * kNW * 8;
-                if (bw < total) {  // uniform: the whole wavefront runs the shuffles
-                    const Q80Lane r = q80_quant_8lanes(v[j]);
-                    const uint32_t b = bw + (lane >> 3);
-                    if (b < total) q80_store(lds + (b / nb) * A.row_bytes, A, b % nb, sub, r);
-                }
+        for (int j = 0; j < kBatch; j++) {
+            // unconditional loads, clamped to the last live block (rows past
+            // mcount quantize copies of it; their outputs are never stored)
+            const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * (kq ? k / 256 : k / 32);
+            if (kq) {
+                const uint32_t nb = k / 256, b = b0 + j * kNW, bc = min(b, live - 1);
+                const float4 t = reinterpret_cast<const float4*>(x + (size_t)(m0 + bc / nb) * k + (bc % nb) * 256)[lane];
+                v[j] = t;
+            } else {
+                const uint32_t nb = k / 32, b = b0 + j * kNW * 8 + (lane >> 3), bc = min(b, live - 1);
+                const float4 t = reinterpret_cast<const float4*>(x + (size_t)(m0 + bc / nb) * k + (bc % nb) * 32)[lane & 7];
+                v[j] = t;
             }
         }
     }
-}
+    // Every block slot is quantized, also past the end (on clamped copies),
+    // and only the store is conditional: a loaded value used only under a
+    // condition would have its load moved behind the weight loads.
+    __device__ __forceinline__ void quant(uint8_t* lds, const ActImg& A, uint32_t k, uint32_t b0, uint32_t lane) {
+        const uint32_t tot = total(k);
+#pragma unroll
+        for (int j = 0; j < kBatch; j++) {
+            if (kq) {
+                const uint32_t nb = k / 256, b = b0 + j * kNW;
+                const Q8KLane r = q8k_quant_wave(v[j], (int)lane);
+                if (b < tot) q8k_store(lds + (b / nb) * A.row_bytes, A, b % nb, (int)lane, r);  // uniform
+            } else {
+                const uint32_t nb = k / 32, b = b0 + j * kNW * 8 + (lane >> 3);
+                const Q80Lane r = q80_quant_8lanes(v[j]);
+                if (b < tot) q80_store(lds + (b / nb) * A.row_bytes, A, b % nb, (int)(lane & 7), r);
+            }
+        }
+    }
+    // the rounds after the first
+    __device__ __forceinline__ void rest(const float* __restrict__ x, uint32_t k, uint32_t m0, uint32_t mcount,
+                                         uint8_t* lds, const ActImg& A, uint32_t wave, uint32_t lane) {
+        for (uint32_t b0 = first(wave) + step(); b0 < total(k); b0 += step()) {
+            load(x, k, m0, mcount, b0, lane);
+            quant(lds, A, k, b0, lane);
+        }
+    }
+};
 
 // Per-chunk weight data held in registers between the load and the compute.
 struct Chunk {
@@ -234,11 +242,12 @@ struct StagePrefetch {
     __device__ __forceinline__ void load(const AView& a, uint32_t m0, uint32_t mcount) {
         const uint32_t rb = a.A.row_bytes;
         const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * rb / 16;
+        const uint32_t total = (uint32_t)MB * rb / 16;
         const uint4* src = reinterpret_cast<const uint4*>(a.img + (size_t)m0 * rb);
 #pragma unroll
         for (int j = 0; j < kPer; j++) {
             const uint32_t i = j * NW * kWave + threadIdx.x;
-            v[j] = i < live ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+            v[j] = src[min(min(i, total - 1), live - 1)];
         }
     }
     // Write the prefetched batch and copy whatever it did not cover.
@@ -247,10 +256,15 @@ struct StagePrefetch {
         const uint32_t total = (uint32_t)MB * rb / 16;
         const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * rb / 16;
         uint4* dst = reinterpret_cast<uint4*>(lds);
+        // Unconditional stores of unconditional loads (a load whose value is
+        // used only under a condition gets moved behind the weight loads by
+        // the compiler).  Lanes past the end rewrite the last slot with the
+        // value it gets anyway; rows past mcount hold copies of the last live
+        // data, whose outputs are never stored.
 #pragma unroll
         for (int j = 0; j < kPer; j++) {
-            const uint32_t i = j * NW * kWave + threadIdx.x;
-            if (i < total) dst[i] = v[j];
+            const uint32_t i = min(j * NW * kWave + threadIdx.x, total - 1);
+            dst[i] = v[j];
         }
         const uint4* src = reinterpret_cast<const uint4*>(a.img + (size_t)m0 * rb);
         for (uint32_t i = kPer * NW * kWave + threadIdx.x; i < total; i += NW * kWave)
@@ -274,15 +288,19 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     const uint32_t gstride = gridDim.x * NW;
     uint32_t g = blockIdx.x * NW + wave;
 
+    // Loads are unconditional (row and chunk clamped to the last valid one,
+    // results past the end are never used): with no branches around them the
+    // compiler counts outstanding loads exactly and waits for the activation
+    // data without waiting for the weight stream behind it.
     Chunk ch[R][CPL];
     auto issue = [&](uint32_t grp, uint32_t pass) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t row = grp * R + r;
+            const uint32_t row = min(grp * R + r, w.n - 1);
 #pragma unroll
             for (int v = 0; v < CPL; v++) {
-                const uint32_t c = lane + 64 * (v + CPL * pass);
-                if (row < w.n && c < nchunks) load_chunk<DT>(w, row, c, ch[r][v]);
+                const uint32_t c = min(lane + 64 * (v + CPL * pass), nchunks - 1);
+                load_chunk<DT>(w, row, c, ch[r][v]);
             }
         }
     };
@@ -291,10 +309,16 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     // whole first row group; the activation image is built while the weight
     // loads travel.
     StagePrefetch<MB, NW> pre;
-    if (!FUSED) pre.load(a, m0, mcount);
-    if (g < ngroups) issue(g, 0);
-    if (FUSED) quantize_into_lds<DT, MB, NW>(x, w.k, m0, mcount, lds);
-    else pre.store(a, m0, mcount, lds);
+    XQuant<DT, MB, NW, 4> xq;
+    if (FUSED) xq.load(x, w.k, m0, mcount, xq.first(wave), lane);
+    else pre.load(a, m0, mcount);
+    issue(min(g, ngroups - 1), 0);
+    if (FUSED) {
+        xq.quant(lds, A, w.k, xq.first(wave), lane);
+        xq.rest(x, w.k, m0, mcount, lds, A, wave, lane);
+    } else {
+        pre.store(a, m0, mcount, lds);
+    }
     __syncthreads();
 
     for (; g < ngroups; g += gstride) {
@@ -329,6 +353,76 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
         if (lane < (uint32_t)(R * MB) && i < mcount && g * R + r < w.n)
             y[(size_t)(m0 + i) * w.n + g * R + r] = out;
     }
+}
+
+// One activation row (m == 1, the decode step): every wavefront owns R
+// consecutive weight rows and there is no grid-stride loop, so the kernel is
+// straight-line code: the activation loads, then every weight load of the
+// wavefront's R rows (K <= 64 * CPL * 32; longer rows take further passes),
+// then the activation image is built in LDS while the weight stream is in
+// flight.  The host picks R so the whole grid is resident at once where it
+// can, which puts the whole weight matrix in flight from the start.
+template <int DT, int R, int CPL, int NW, bool FUSED>
+__global__ __launch_bounds__(NW * 64) void stream_kernel(WView w, AView a, const float* __restrict__ x,
+                                                         float* __restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    const ActImg A = act_img(w.k, kq);
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t nchunks = w.k / 32;
+    const uint32_t npass = (nchunks + 64 * CPL - 1) / (64 * CPL);
+    const uint32_t row0 = (blockIdx.x * NW + wave) * R;
+
+    Chunk ch[R][CPL];
+    auto issue = [&](uint32_t pass) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = min(row0 + r, w.n - 1);
+#pragma unroll
+            for (int v = 0; v < CPL; v++)
+                load_chunk<DT>(w, row, min(lane + 64 * (v + CPL * pass), nchunks - 1), ch[r][v]);
+        }
+    };
+
+    StagePrefetch<1, NW> pre;
+    XQuant<DT, 1, NW, (CPL * 64 + NW * 128 - 1) / (NW * 128)> xq;  // one round covers K = 64 * CPL * 32
+    if (FUSED) xq.load(x, w.k, 0, 1, xq.first(wave), lane);
+    else pre.load(a, 0, 1);
+    issue(0);
+    if (FUSED) {
+        xq.quant(lds, A, w.k, xq.first(wave), lane);
+        xq.rest(x, w.k, 0, 1, lds, A, wave, lane);
+    } else {
+        pre.store(a, 0, 1, lds);
+    }
+    __syncthreads();
+
+    float acc[R][1];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r][0] = 0.0f;
+    for (uint32_t p = 0; p < npass; p++) {
+        if (p > 0) issue(p);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int v = 0; v < CPL; v++) {
+                const uint32_t c = lane + 64 * (v + CPL * p);
+                if (c < nchunks) compute_chunk<DT, 1>(ch[r][v], c, w.k, lds, A, acc[r]);
+            }
+    }
+    float out = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float t = wave_sum(acc[r][0]);
+        if (lane == (uint32_t)r) out = t;
+    }
+    if (lane < (uint32_t)R && row0 + lane < w.n) y[row0 + lane] = out;
+}
+
+inline int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
 }
 
 // Occupancy (workgroups per CU) of one kernel at one LDS size, cached.
@@ -373,13 +467,89 @@ hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m
     return hipGetLastError();
 }
 
-inline int pick_cpl(uint32_t nchunks) {
-    return nchunks <= 64 ? 1 : nchunks <= 128 ? 2 : nchunks <= 256 ? 4 : 8;
+template <int DT, int R, int CPL, int NW, bool FUSED>
+hipError_t launch_stream_one(const WView& w, const AView& a, const float* x, float* y, hipStream_t s,
+                             bool probe, int* fits) {
+    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    const uint32_t lds = lds_bytes(1, w.k, kq);
+    auto fn = stream_kernel<DT, R, CPL, NW, FUSED>;
+    const uint32_t grid = (w.n + R * NW - 1) / (R * NW);
+    if (probe) {
+        int ncu = 1;
+        const int occ = wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);
+        *fits = grid <= (uint32_t)(occ * ncu);
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, w, a, x, y);
+    return hipGetLastError();
 }
 
-inline int env_int(const char* name, int dflt) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : dflt;
+template <int DT, int R, bool FUSED>
+hipError_t launch_stream_r(int cpl, const WView& w, const AView& a, const float* x, float* y, hipStream_t s,
+                           bool probe, int* fits) {
+    // The fused kernel quantizes the whole activation row once per
+    // workgroup, so it uses large workgroups (16 wavefronts, one per CU at the
+    // common shapes); the staging copy of the other is cheap, so 4.
+    constexpr int NW = FUSED ? 16 : 4;
+    // R * CPL is bounded so the weight registers fit without spilling
+    // (128 VGPRs at 16 wavefronts per workgroup)
+    constexpr int kMaxCpl = R == 1 ? 8 : R == 2 ? 5 : 2;
+    switch (cpl) {
+    case 1: return launch_stream_one<DT, R, 1, NW, FUSED>(w, a, x, y, s, probe, fits);
+    case 2: return launch_stream_one<DT, R, 2, NW, FUSED>(w, a, x, y, s, probe, fits);
+    }
+    if constexpr (kMaxCpl >= 5) {
+        switch (cpl) {
+        case 3: return launch_stream_one<DT, R, 3, NW, FUSED>(w, a, x, y, s, probe, fits);
+        case 4: return launch_stream_one<DT, R, 4, NW, FUSED>(w, a, x, y, s, probe, fits);
+        case 5: return launch_stream_one<DT, R, 5, NW, FUSED>(w, a, x, y, s, probe, fits);
+        }
+    }
+    if constexpr (kMaxCpl >= 8) {
+        switch (cpl) {
+        case 6: return launch_stream_one<DT, R, 6, NW, FUSED>(w, a, x, y, s, probe, fits);
+        case 7: return launch_stream_one<DT, R, 7, NW, FUSED>(w, a, x, y, s, probe, fits);
+        default: return launch_stream_one<DT, R, 8, NW, FUSED>(w, a, x, y, s, probe, fits);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+// m == 1: chunks per lane cover the row in one pass up to K = 16384.  Rows
+// per wavefront: the fused kernel takes R = 2 once one 16-wavefront
+// workgroup per CU no longer covers the matrix with R = 1 (fewer workgroups
+// quantize the activation fewer times; R = 4 measured slower), the other the
+// smallest R in {1, 2} whose grid is resident at once.  XNQ_MV_STREAM_ROWS
+// forces R (tuning).
+template <int DT, bool FUSED>
+hipError_t launch_stream(const WView& w, const AView& a, const float* x, float* y, hipStream_t s) {
+    const uint32_t nchunks = w.k / 32;
+    const int cpl = (int)std::min<uint32_t>(8, (nchunks + 63) / 64);
+    static const int forced = env_int("XNQ_MV_STREAM_ROWS", 0);
+    int r = forced;
+    if ((r == 2 && cpl > 5) || (r == 4 && cpl > 2)) r = 0;
+    if (r != 1 && r != 2 && (r != 4 || !FUSED)) {
+        if (FUSED) {  // R within the register bounds of launch_stream_r
+            int ncu = 1;
+            (void)wg_per_cu(reinterpret_cast<const void*>(stream_kernel<DT, 1, 1, 16, true>), 1024, 0, &ncu);
+            const uint32_t waves = (uint32_t)ncu * 16;
+            r = (w.n <= waves || cpl > 5) ? 1 : 2;  // R = 4 measured slower at 14336 rows
+        } else {
+            int fits = 0;
+            hipError_t e = launch_stream_r<DT, 1, FUSED>(cpl, w, a, x, y, s, true, &fits);
+            if (e != hipSuccess) return e;
+            r = fits ? 1 : 2;
+        }
+    }
+    if (r == 1) return launch_stream_r<DT, 1, FUSED>(cpl, w, a, x, y, s, false, nullptr);
+    if constexpr (FUSED) {
+        if (r == 4) return launch_stream_r<DT, 4, FUSED>(cpl, w, a, x, y, s, false, nullptr);
+    }
+    return launch_stream_r<DT, 2, FUSED>(cpl, w, a, x, y, s, false, nullptr);
+}
+
+inline int pick_cpl(uint32_t nchunks) {
+    return nchunks <= 64 ? 1 : nchunks <= 128 ? 2 : nchunks <= 256 ? 4 : 8;
 }
 
 // Decode kernels read a quantized workspace (4 wavefronts per workgroup,
@@ -391,6 +561,21 @@ hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const floa
     constexpr int NW = FUSED ? 16 : 4;
 #define XNQ_MV(RR, CC)                                                          \
     if (R == RR && cpl == CC) return launch_one<DT, MB, RR, CC, NW, FUSED>(w, a, x, m0, mc, y, s);
+    if constexpr (MB == 1 && FUSED) {
+        static const int fnw = env_int("XNQ_MV_FUSED_NW", 16);
+        if (R == 1 && fnw == 4) {
+            if (cpl == 1) return launch_one<DT, MB, 1, 1, 4, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 2) return launch_one<DT, MB, 1, 2, 4, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 4) return launch_one<DT, MB, 1, 4, 4, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 8) return launch_one<DT, MB, 1, 8, 4, FUSED>(w, a, x, m0, mc, y, s);
+        }
+        if (R == 1 && fnw == 8) {
+            if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 8) return launch_one<DT, MB, 1, 8, 8, FUSED>(w, a, x, m0, mc, y, s);
+        }
+    }
     if constexpr (MB == 1) {
         XNQ_MV(1, 1) XNQ_MV(2, 1) XNQ_MV(4, 1) XNQ_MV(1, 2) XNQ_MV(2, 2) XNQ_MV(4, 2)
         XNQ_MV(1, 4) XNQ_MV(2, 4) XNQ_MV(1, 8)
@@ -425,7 +610,10 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
     for (size_t m0 = 0; m0 < m; m0 += gmax) {
         const uint32_t mc = (uint32_t)((m - m0) < (size_t)gmax ? (m - m0) : (size_t)gmax);
         hipError_t e;
-        if (fused) {
+        static const bool legacy = env_int("XNQ_MV_LEGACY", 0) != 0;
+        if (mc == 1 && m == 1 && fused && !legacy) {
+            e = launch_stream<DT, true>(w, a, x, y, s);
+        } else if (fused) {
             if (mc == 1) e = launch_cpl<DT, 1, true>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
             else if (mc == 2) e = launch_cpl<DT, 2, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
             else if (mc <= 4) e = launch_cpl<DT, 4, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);

@@ -196,7 +196,7 @@ extern "C" {
 
 const char* xnq_last_error(void) { return g_err.c_str(); }
 
-int xnq_abi_version(void) { return 2; }
+int xnq_abi_version(void) { return 3; }
 
 size_t xnq_type_size(uint32_t dtype) { return type_size(dtype); }
 size_t xnq_block_size(uint32_t dtype) { return block_size(dtype); }
@@ -414,8 +414,20 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     return XNQ_OK;
 }
 
-xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
-                                const float* lhs_dev, float* dst_dev, void* stream) {
+// Decode: the matvec route for up to 8 rows quantizes the activation rows in
+// LDS inside the matvec kernels and needs no workspace.
+static bool fused_route(const xnq_qtensor* qt, size_t m) {
+    const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k);
+    return r == kMatvec && (m <= 8 || g_route.load() == 1);
+}
+
+size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m) {
+    if (!qt || fused_route(qt, m)) return 0;
+    return xnq_qtensor_workspace_size(qt, m);
+}
+
+xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, size_t n, const float* lhs_dev,
+                                   void* workspace_dev, size_t workspace_bytes, float* dst_dev, void* stream) {
     xnq_status st = check_mkn(qt, m, k, n);
     if (st) return st;
     st = check_lhs(qt->L.dtype, k);
@@ -425,10 +437,7 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
-    const Route r = pick_route(qt->L.dtype, m, n, k);
-    if (r == kMatvec && (m <= 8 || g_route.load() == 1)) {
-        // Decode: each launch quantizes its (up to 8) rows in LDS and streams
-        // the weight; no workspace.
+    if (fused_route(qt, m)) {
         const WView w = make_wview(qt->L, qt->buf);
         hipError_t e = launch_matvec_fused(w, lhs_dev, m, dst_dev, s);
         if (e == hipErrorInvalidConfiguration)
@@ -436,12 +445,28 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
         if (e != hipSuccess) return hip_fail(e, "matvec kernel");
         return XNQ_OK;
     }
-    const size_t ws_bytes = xnq_qtensor_workspace_size(qt, m);
+    const size_t need = act_layout(qt->L.dtype, m, k).bytes;
+    if (!workspace_dev || workspace_bytes < need)
+        return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu the activation needs",
+                    workspace_bytes, need);
+    st = xnq_quantize_lhs(qt->L.dtype, m, k, lhs_dev, workspace_dev, stream);
+    if (!st) st = xnq_qtensor_matmul_preq(qt, m, k, n, workspace_dev, workspace_bytes, dst_dev, stream);
+    return st;
+}
+
+xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                const float* lhs_dev, float* dst_dev, void* stream) {
+    xnq_status st = check_mkn(qt, m, k, n);
+    if (st) return st;
+    const size_t ws_bytes = xnq_qtensor_matmul_t_workspace_size(qt, m);
+    if (ws_bytes == 0 || n == 0 || m == 0) return xnq_qtensor_matmul_t_ws(qt, m, k, n, lhs_dev, nullptr, 0, dst_dev, stream);
+    DeviceGuard g(qt->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t s = (hipStream_t)stream;
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, ws_bytes, s);
     if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(workspace)");
-    st = xnq_quantize_lhs(qt->L.dtype, m, k, lhs_dev, ws, stream);
-    if (!st) st = xnq_qtensor_matmul_preq(qt, m, k, n, ws, ws_bytes, dst_dev, stream);
+    st = xnq_qtensor_matmul_t_ws(qt, m, k, n, lhs_dev, ws, ws_bytes, dst_dev, stream);
     (void)hipFreeAsync(ws, s);
     return st;
 }

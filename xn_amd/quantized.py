@@ -255,18 +255,31 @@ class QTensor:
     def matmul_t(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
         """dst[m, n] = quantize(lhs[m, k]) . W^T (mod.rs:334-339, k_quants.rs:1996-2011).
 
-        The quantized activation goes to a workspace from torch's caching
-        allocator (graph-capture safe, no per-call device allocation), then
-        the library's quantize_lhs and matmul_preq run on the current stream:
-        quantize_lhs + T::matmul, as k_quants::matmul does."""
+        Decode-sized m (the matvec route) is one kernel that quantizes the
+        rows in LDS; otherwise the quantized activation goes to a workspace
+        from torch's caching allocator (graph-capture safe, no per-call
+        device allocation) and the library runs quantize_lhs + T::matmul, as
+        k_quants::matmul does.  Runs on the current stream."""
         m, k, n = self._check_mm(mkn, lhs, dst)
         if m == 0 or n == 0:
             return
-        dt = self.dtype()
+        L = _lib.load()
+        h = self.storage.handle
+        nbytes = L.xnq_qtensor_matmul_t_workspace_size(h, m)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device) if nbytes else None
+        check(L.xnq_qtensor_matmul_t_ws(h, m, k, n, _ptr(lhs), _ptr(ws) if ws is not None else None, nbytes,
+                                        _ptr(dst), _stream(self.device)))
+
+    def matmul_t_split(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
+        """quantize_lhs then matmul_preq as two library calls, for every m
+        (k_quants.rs:2014-2026: quantize_lhs, then T::matmul)."""
+        m, k, n = self._check_mm(mkn, lhs, dst)
+        if m == 0 or n == 0:
+            return
         ws = self.workspace(m)
         L = _lib.load()
         st = _stream(self.device)
-        check(L.xnq_quantize_lhs(int(dt), m, k, _ptr(lhs), _ptr(ws), st))
+        check(L.xnq_quantize_lhs(int(self.dtype()), m, k, _ptr(lhs), _ptr(ws), st))
         check(L.xnq_qtensor_matmul_preq(self.storage.handle, m, k, n, _ptr(ws), ws.numel(), _ptr(dst), st))
 
     def workspace(self, m: int) -> torch.Tensor:
