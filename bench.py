@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=512)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "sweep"], default="all",
+    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "sweep", "decode"], default="all",
                    help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters); "
                         "'sweep' times every configured shape (matvec sweep, FFN, prefill, decode step)")
     p.add_argument("--eager", action="store_true",
@@ -127,7 +127,9 @@ def sweep(args, dev, stream, gen) -> dict:
     import torch
 
     from xn_amd import GgmlDType, QTensor
-    from xn_amd.quantized import lhs_workspace, matmul_preq, quantize_lhs
+    from xn_amd.quantized import matmul_preq, matmul_t_group, matmul_t_silu_gate, quantize_lhs
+
+    decode_only = args.only == "decode"
 
     def make(dt, n, k):
         w = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * 0.02
@@ -172,15 +174,16 @@ def sweep(args, dev, stream, gen) -> dict:
             print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
         del ws
 
-    # config 1: Q8_0 4096 -> 4096
-    matvec_row("1 q8_0 matvec", 8, 4096, 4096, [1])
-    # config 3: Q4_K sweep
-    for k, n in [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 28672)]:
-        matvec_row("3 q4k sweep", 12, k, n, [1, 2, 4, 8])
-    # the other decode dtypes at the FFN shapes
-    matvec_row("5 q6k ffn down", 14, 14336, 4096, [1, 4])
-    matvec_row("2 q4_0 gate/up", 2, 4096, 14336, [1])
-    matvec_row("2 q4_0 down", 2, 14336, 4096, [1])
+    if not decode_only:
+        # config 1: Q8_0 4096 -> 4096
+        matvec_row("1 q8_0 matvec", 8, 4096, 4096, [1])
+        # config 3: Q4_K sweep
+        for k, n in [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 28672)]:
+            matvec_row("3 q4k sweep", 12, k, n, [1, 2, 4, 8])
+        # the other decode dtypes at the FFN shapes
+        matvec_row("5 q6k ffn down", 14, 14336, 4096, [1, 4])
+        matvec_row("2 q4_0 gate/up", 2, 4096, 14336, [1])
+        matvec_row("2 q4_0 down", 2, 14336, 4096, [1])
 
     # config 2: Q4_0 FFN block, h = silu(x Wg^T) * (x Wu^T), y = h Wd^T
     k, f = 4096, 14336
@@ -198,16 +201,23 @@ def sweep(args, dev, stream, gen) -> dict:
         torch.mul(torch.nn.functional.silu(g_), u_, out=h_)
         wd.matmul_t((1, f, k), h_, y_)
 
-    ms = timed(ffn, steps)
+    def ffn_fused(i):
+        wg, wu, wd = sets[i % len(sets)]
+        matmul_t_silu_gate(wg, wu, (1, k, f), x, h_)
+        wd.matmul_t((1, f, k), h_, y_)
+
     algo = 3 * qbytes(2, f, k) + (2 * k + 3 * f) * 4 + f * 4
-    rows.append({"config": "2 q4_0 ffn block (silu gate, torch elementwise)", "m": 1, "us_step": round(ms * 1e3, 2),
-                 "gbs_step": round(algo / (ms * 1e-3) / 1e9, 1)})
-    print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    for name, fn in (("2 q4_0 ffn block (gate, up, torch SiLU-mul, down)", ffn),
+                     ("2 q4_0 ffn block (fused SiLU-gated gate/up kernel, down)", ffn_fused)):
+        ms = timed(fn, steps)
+        rows.append({"config": name, "m": 1, "us_step": round(ms * 1e3, 2),
+                     "gbs_step": round(algo / (ms * 1e-3) / 1e9, 1)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
     del sets
 
     # config 4: prefill on int8 MFMA
     k, n = 4096, 14336
-    for dt in (12, 14):
+    for dt in (() if decode_only else (12, 14)):
         ws = [make(dt, n, k) for _ in range(copies_for(qbytes(dt, n, k)))]
         for m in (64, 256, 512, 2048):
             x = torch.randn((m, k), generator=gen, device=dev)
@@ -228,27 +238,42 @@ def sweep(args, dev, stream, gen) -> dict:
 
     # config 5: every QMatMul of one decode step (random weights; attention itself is out of scope)
     d, kv, ff, vocab, layers = 4096, 1024, 14336, 128256, 32
-    mats = []
+    mats, layer_w = [], []
     for _ in range(layers):
-        mats += [(make(12, d, d), d, d), (make(12, kv, d), d, kv), (make(12, kv, d), d, kv),
-                 (make(12, d, d), d, d), (make(12, ff, d), d, ff), (make(12, ff, d), d, ff),
-                 (make(14, d, ff), ff, d)]
-    mats.append((make(14, vocab, d), d, vocab))
+        lw = [make(12, d, d), make(12, kv, d), make(12, kv, d), make(12, d, d), make(12, ff, d), make(12, ff, d),
+              make(14, d, ff)]
+        layer_w.append(lw)
+        mats += [(lw[0], d, d), (lw[1], d, kv), (lw[2], d, kv), (lw[3], d, d), (lw[4], d, ff), (lw[5], d, ff),
+                 (lw[6], ff, d)]
+    head = make(14, vocab, d)
+    mats.append((head, d, vocab))
     wtotal = sum(qbytes(12 if q.dtype() == GgmlDType.Q4K else 14, n, kk) for q, kk, n in mats)
     for b in (1, 16):
         xs = {kk: torch.randn((b, kk), generator=gen, device=dev) for kk in (d, ff)}
         ys = {n: torch.empty((b, n), device=dev) for n in (d, kv, ff, vocab)}
+        yk = torch.empty((b, kv), device=dev)
 
         def step(i):
             for q, kk, n in mats:
                 q.matmul_t((b, kk, n), xs[kk], ys[n])
 
-        ms = timed(step, 3)
-        rows.append({"config": "5 decode step (225 QMatMuls)", "batch": b, "weight_bytes": wtotal,
-                     "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
-                     "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
-        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
-    del mats
+        def step_grouped(i):
+            # q, k, v in one launch; gate and up with the SiLU gate in one launch
+            for lw in layer_w:
+                matmul_t_group(lw[0:3], b, d, xs[d], [ys[d], ys[kv], yk])
+                lw[3].matmul_t((b, d, d), xs[d], ys[d])
+                matmul_t_silu_gate(lw[4], lw[5], (b, d, ff), xs[d], ys[ff])
+                lw[6].matmul_t((b, ff, d), xs[ff], ys[d])
+            head.matmul_t((b, d, vocab), xs[d], ys[vocab])
+
+        for name, fn in (("5 decode step (225 QMatMuls, one call each)", step),
+                         ("5 decode step (q/k/v grouped, SiLU-gated gate/up)", step_grouped)):
+            ms = timed(fn, 3)
+            rows.append({"config": name, "batch": b, "weight_bytes": wtotal,
+                         "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    del mats, layer_w
     return {"metric": "per-config sweep", "rows": rows}
 
 
@@ -298,7 +323,7 @@ def main():
                           "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}), flush=True)
         return
 
-    if args.only == "sweep":
+    if args.only in ("sweep", "decode"):
         print(json.dumps(sweep(args, dev, stream, gen)), flush=True)
         return
 

@@ -112,6 +112,30 @@ xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, si
                                    const float* lhs_dev, void* workspace_dev, size_t workspace_bytes,
                                    float* dst_dev, void* stream);
 
+/* Decode-step groups (no reference entry point of their own: they compute
+ * what two or three QMatMul calls on one activation compute, in one launch
+ * for m == 1).
+ *
+ * silu_gate: dst[m x n] = silu(lhs . gate^T) * (lhs . up^T), the SwiGLU of
+ * llama.rs:258-264 (Mlp::forward) with silu(s) = s / (1 + exp(0 - s))
+ * (cpu_backend.rs:354-356); gate and up have one shape.  m == 1 with both on
+ * the decode route and K <= 10240 is one kernel and needs no workspace;
+ * otherwise the two products go through matmul_t_ws and a SiLU-multiply
+ * kernel, with workspace for the second product.
+ *
+ * group: dsts[i][m x n_i] = lhs . qts[i]^T for up to 3 weights of one dtype
+ * and K (the q, k, v projections of llama.rs:156-158); m == 1 on the decode
+ * route is one kernel over the joined rows, other cases one matmul_t_ws per
+ * weight.  Workspace sizes are 0 when the single-kernel route applies. */
+size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m);
+xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
+                                  const float* lhs_dev, void* workspace_dev, size_t workspace_bytes,
+                                  float* dst_dev, void* stream);
+size_t xnq_matmul_t_group_workspace_size(const xnq_qtensor* const* qts, size_t count, size_t m);
+xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
+                              const float* lhs_dev, float* const* dsts_dev, void* workspace_dev,
+                              size_t workspace_bytes, void* stream);
+
 /* The two halves of matmul_t, for callers that keep the quantized
  * activation around or manage the scratch memory themselves
  * (k_quants.rs:2014-2026 quantize_lhs, then T::matmul).  The workspace

@@ -253,3 +253,58 @@ def test_errors(orc, dev):
         qt.matmul_t((2, 256, 4), lhs[:100], dst)
     # m = 0 is a no-op
     qt.matmul_t((0, 256, 4), lhs[:0], dst[:0])
+
+
+# ------------------------------------------------ decode-step groups
+def _silu(v):
+    return v / (1.0 + np.exp(0.0 - v))
+
+
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+@pytest.mark.parametrize("m,k,n", [(1, 2048, 300), (1, 4096, 1000), (3, 2048, 300), (1, 12288, 96), (9, 1024, 64)])
+def test_silu_gate(orc, dev, dt, m, k, n):
+    """SwiGLU of llama.rs:258-264: silu(x . gate) * (x . up), one kernel at m = 1."""
+    from xn_amd.quantized import matmul_t_silu_gate
+
+    rng = np.random.default_rng(8100 + dt + m + k + n)
+    gb = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    ub = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    g, u = upload(gb, n, k, dt, dev), upload(ub, n, k, dt, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    matmul_t_silu_gate(g, u, (m, k, n), torch.from_numpy(x).to(dev), dst)
+    want = _silu(orc.matmul(dt, x, gb, n).astype(np.float64)) * orc.matmul(dt, x, ub, n)
+    assert_close(dst.cpu().numpy(), want, f"silu_gate dt={dt} m={m} k={k} n={n}")
+
+
+@pytest.mark.parametrize("dt", WEIGHT_DTYPES)
+@pytest.mark.parametrize("m,ns", [(1, (300,)), (1, (512, 128, 128)), (1, (40, 7)), (2, (200, 64, 64))])
+def test_matmul_group(orc, dev, dt, m, ns):
+    """q, k, v projections of one activation (llama.rs:156-158) in one launch."""
+    from xn_amd.quantized import matmul_t_group
+
+    k = 2048
+    rng = np.random.default_rng(8200 + dt + m + sum(ns))
+    blocks = [orc.from_float(dt, rng.normal(0, 0.02, (n, k))) for n in ns]
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qts = [upload(b, n, k, dt, dev) for b, n in zip(blocks, ns)]
+    dsts = [torch.full((m, n), float("nan"), dtype=torch.float32, device=dev) for n in ns]
+    matmul_t_group(qts, m, k, torch.from_numpy(x).to(dev), dsts)
+    for i, (b, n) in enumerate(zip(blocks, ns)):
+        assert_close(dsts[i].cpu().numpy(), orc.matmul(dt, x, b, n), f"group dt={dt} m={m} weight {i} n={n}")
+
+
+def test_matmul_group_mixed_dtypes(orc, dev):
+    """Weights of different dtypes share no kernel: one matmul per weight."""
+    from xn_amd.quantized import matmul_t_group
+
+    k = 1024
+    rng = np.random.default_rng(8300)
+    specs = [(Q4K, 96), (Q6K, 64), (Q8_0, 32)]
+    blocks = [orc.from_float(dt, rng.normal(0, 0.02, (n, k))) for dt, n in specs]
+    x = rng.normal(0, 1, (1, k)).astype(np.float32)
+    qts = [upload(b, n, k, dt, dev) for b, (dt, n) in zip(blocks, specs)]
+    dsts = [torch.empty((1, n), dtype=torch.float32, device=dev) for _, n in specs]
+    matmul_t_group(qts, 1, k, torch.from_numpy(x).to(dev), dsts)
+    for d, b, (dt, n) in zip(dsts, blocks, specs):
+        assert_close(d.cpu().numpy(), orc.matmul(dt, x, b, n), f"mixed group dt={dt}")

@@ -38,6 +38,11 @@ SIGNATURES = {
     "xnq_qtensor_matmul_t": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_void]),
     "xnq_qtensor_matmul_t_workspace_size": (c_size, [c_void, c_size]),
     "xnq_qtensor_matmul_t_ws": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void]),
+    "xnq_matmul_t_silu_gate_workspace_size": (c_size, [c_void, c_void, c_size]),
+    "xnq_matmul_t_silu_gate": (c_int, [c_void, c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void]),
+    "xnq_matmul_t_group_workspace_size": (c_size, [ctypes.POINTER(c_void), c_size, c_size]),
+    "xnq_matmul_t_group": (c_int, [ctypes.POINTER(c_void), c_size, c_size, c_size, c_void, ctypes.POINTER(c_void), c_void,
+                                   c_size, c_void]),
     "xnq_lhs_workspace_size": (c_size, [c_u32, c_size, c_size]),
     "xnq_qtensor_workspace_size": (c_size, [c_void, c_size]),
     "xnq_quantize_lhs": (c_int, [c_u32, c_size, c_size, c_void, c_void, c_void]),

@@ -57,7 +57,22 @@ __global__ void block_ints_kernel(WView w, AView a, uint32_t m, int32_t* __restr
     out[2 * t + 1] = r1;
 }
 
+// g = silu(g) * u, silu(s) = s / (1 + exp(0 - s)) (cpu_backend.rs:354-356)
+__global__ __launch_bounds__(256) void silu_mul_kernel(float* __restrict__ g, const float* __restrict__ u,
+                                                       size_t count) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    const float t = g[i];
+    g[i] = t / (1.0f + expf(0.0f - t)) * u[i];
+}
+
 }  // namespace
+
+hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    silu_mul_kernel<<<(unsigned)((count + 255) / 256), 256, 0, s>>>(g, u, count);
+    return hipGetLastError();
+}
 
 hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hipStream_t s) {
     switch (w.dtype) {
@@ -79,6 +94,16 @@ hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* 
     case XNQ_Q4_0: return launch_matvec_q4_0(w, a, x, m, y, s, true);
     case XNQ_Q4K: return launch_matvec_q4k(w, a, x, m, y, s, true);
     case XNQ_Q6K: return launch_matvec_q6k(w, a, x, m, y, s, true);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_matvec_group(const WGroup& g, const float* x, bool gate, hipStream_t s) {
+    switch (g.w[0].dtype) {
+    case XNQ_Q8_0: return launch_group_q8_0(g, x, gate, s);
+    case XNQ_Q4_0: return launch_group_q4_0(g, x, gate, s);
+    case XNQ_Q4K: return launch_group_q4k(g, x, gate, s);
+    case XNQ_Q6K: return launch_group_q6k(g, x, gate, s);
     }
     return hipErrorInvalidValue;
 }

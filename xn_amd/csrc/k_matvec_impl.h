@@ -355,69 +355,112 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     }
 }
 
-// One activation row (m == 1, the decode step): every wavefront owns R
-// consecutive weight rows and there is no grid-stride loop, so the kernel is
-// straight-line code: the activation loads, then every weight load of the
-// wavefront's R rows (K <= 64 * CPL * 32; longer rows take further passes),
-// then the activation image is built in LDS while the weight stream is in
-// flight.  The host picks R so the whole grid is resident at once where it
-// can, which puts the whole weight matrix in flight from the start.
-template <int DT, int R, int CPL, int NW, bool FUSED>
-__global__ __launch_bounds__(NW * 64) void stream_kernel(WView w, AView a, const float* __restrict__ x,
-                                                         float* __restrict__ y) {
+// One activation row (m == 1, the decode step), f32 activation quantized in
+// LDS by every workgroup, over a group of weights that share it:
+//   plain / grouped: the rows of up to kMaxGroup weights (same dtype and K,
+//     e.g. the q, k and v projections, llama.rs:156-158) form one row space;
+//     each output row goes to its own weight's destination;
+//   GATE: two weights of the same shape (gate, up), one output
+//     y = silu(x . gate) * (x . up), the SwiGLU of llama.rs:258-264 with
+//     silu(s) = s / (1 + exp(0 - s)) (cpu_backend.rs:354-356).
+// Every wavefront owns R rows (GATE: R rows of each weight) and there is no
+// grid-stride loop, so the kernel is straight-line code: the activation
+// loads, then every weight load of the wavefront's rows (K <= 64 * CPL * 32;
+// longer rows take further passes), then the activation image is built in
+// LDS while the weight stream is in flight.
+template <int DT, int R, int CPL, int NW, bool GATE>
+__global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* __restrict__ x) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
-    const ActImg A = act_img(w.k, kq);
+    constexpr int RR = GATE ? 2 * R : R;  // rows loaded per wavefront
+    const uint32_t k = G.w[0].k;
+    const ActImg A = act_img(k, kq);
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = threadIdx.x / kWave;
-    const uint32_t nchunks = w.k / 32;
+    const uint32_t nchunks = k / 32;
     const uint32_t npass = (nchunks + 64 * CPL - 1) / (64 * CPL);
     const uint32_t row0 = (blockIdx.x * NW + wave) * R;
 
-    Chunk ch[R][CPL];
-    auto issue = [&](uint32_t pass) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint32_t row = min(row0 + r, w.n - 1);
-#pragma unroll
-            for (int v = 0; v < CPL; v++)
-                load_chunk<DT>(w, row, min(lane + 64 * (v + CPL * pass), nchunks - 1), ch[r][v]);
+    // weight t and local row of loaded row r (wavefront-uniform)
+    auto locate = [&](int r, uint32_t& t, uint32_t& lr) {
+        if (GATE) {
+            t = r < R ? 0u : 1u;
+            lr = min(row0 + (uint32_t)(r % R), G.rows - 1);
+            return;
+        }
+        const uint32_t gr = min(row0 + (uint32_t)r, G.rows - 1);
+        t = 0;
+        lr = gr;
+        if (G.count > 1 && gr >= G.row_end[0]) {
+            t = 1;
+            lr = gr - G.row_end[0];
+            if (G.count > 2 && gr >= G.row_end[1]) {
+                t = 2;
+                lr = gr - G.row_end[1];
+            }
         }
     };
 
-    StagePrefetch<1, NW> pre;
+    Chunk ch[RR][CPL];
+    auto issue = [&](uint32_t pass) {
+#pragma unroll
+        for (int r = 0; r < RR; r++) {
+            uint32_t t, lr;
+            locate(r, t, lr);
+            const WView& w = G.w[t];
+#pragma unroll
+            for (int v = 0; v < CPL; v++)
+                load_chunk<DT>(w, lr, min(lane + 64 * (v + CPL * pass), nchunks - 1), ch[r][v]);
+        }
+    };
+
     XQuant<DT, 1, NW, (CPL * 64 + NW * 128 - 1) / (NW * 128)> xq;  // one round covers K = 64 * CPL * 32
-    if (FUSED) xq.load(x, w.k, 0, 1, xq.first(wave), lane);
-    else pre.load(a, 0, 1);
+    xq.load(x, k, 0, 1, xq.first(wave), lane);
     issue(0);
-    if (FUSED) {
-        xq.quant(lds, A, w.k, xq.first(wave), lane);
-        xq.rest(x, w.k, 0, 1, lds, A, wave, lane);
-    } else {
-        pre.store(a, 0, 1, lds);
-    }
+    xq.quant(lds, A, k, xq.first(wave), lane);
+    xq.rest(x, k, 0, 1, lds, A, wave, lane);
     __syncthreads();
 
-    float acc[R][1];
+    float acc[RR][1];
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r][0] = 0.0f;
+    for (int r = 0; r < RR; r++) acc[r][0] = 0.0f;
     for (uint32_t p = 0; p < npass; p++) {
         if (p > 0) issue(p);
 #pragma unroll
-        for (int r = 0; r < R; r++)
+        for (int r = 0; r < RR; r++)
 #pragma unroll
             for (int v = 0; v < CPL; v++) {
                 const uint32_t c = lane + 64 * (v + CPL * p);
-                if (c < nchunks) compute_chunk<DT, 1>(ch[r][v], c, w.k, lds, A, acc[r]);
+                if (c < nchunks) compute_chunk<DT, 1>(ch[r][v], c, k, lds, A, acc[r]);
             }
     }
     float out = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const float t = wave_sum(acc[r][0]);
+        float t = wave_sum(acc[r][0]);
+        if (GATE) {
+            const float u = wave_sum(acc[R + r][0]);
+            t = t / (1.0f + expf(0.0f - t)) * u;
+        }
         if (lane == (uint32_t)r) out = t;
     }
-    if (lane < (uint32_t)R && row0 + lane < w.n) y[row0 + lane] = out;
+    const uint32_t gr = row0 + lane;
+    if (lane < (uint32_t)R && gr < G.rows) {
+        if (GATE) {
+            G.y[0][gr] = out;
+        } else {
+            uint32_t t = 0, lr = gr;
+            if (G.count > 1 && gr >= G.row_end[0]) {
+                t = 1;
+                lr = gr - G.row_end[0];
+                if (G.count > 2 && gr >= G.row_end[1]) {
+                    t = 2;
+                    lr = gr - G.row_end[1];
+                }
+            }
+            G.y[t][lr] = out;
+        }
+    }
 }
 
 inline int env_int(const char* name, int dflt) {
@@ -467,85 +510,66 @@ hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m
     return hipGetLastError();
 }
 
-template <int DT, int R, int CPL, int NW, bool FUSED>
-hipError_t launch_stream_one(const WView& w, const AView& a, const float* x, float* y, hipStream_t s,
-                             bool probe, int* fits) {
+template <int DT, int R, int CPL, bool GATE>
+hipError_t launch_group_one(const WGroup& g, const float* x, hipStream_t s) {
     constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
-    const uint32_t lds = lds_bytes(1, w.k, kq);
-    auto fn = stream_kernel<DT, R, CPL, NW, FUSED>;
-    const uint32_t grid = (w.n + R * NW - 1) / (R * NW);
-    if (probe) {
-        int ncu = 1;
-        const int occ = wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);
-        *fits = grid <= (uint32_t)(occ * ncu);
-        return hipSuccess;
-    }
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, w, a, x, y);
+    constexpr int NW = 16;
+    const uint32_t lds = lds_bytes(1, g.w[0].k, kq);
+    auto fn = group_kernel<DT, R, CPL, NW, GATE>;
+    int ncu = 1;
+    (void)wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);  // sets the LDS limit once
+    const uint32_t grid = (g.rows + R * NW - 1) / (R * NW);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, g, x);
     return hipGetLastError();
 }
 
-template <int DT, int R, bool FUSED>
-hipError_t launch_stream_r(int cpl, const WView& w, const AView& a, const float* x, float* y, hipStream_t s,
-                           bool probe, int* fits) {
-    // The fused kernel quantizes the whole activation row once per
-    // workgroup, so it uses large workgroups (16 wavefronts, one per CU at the
-    // common shapes); the staging copy of the other is cheap, so 4.
-    constexpr int NW = FUSED ? 16 : 4;
-    // R * CPL is bounded so the weight registers fit without spilling
-    // (128 VGPRs at 16 wavefronts per workgroup)
-    constexpr int kMaxCpl = R == 1 ? 8 : R == 2 ? 5 : 2;
+// Rows * chunks per lane are bounded so the weight registers fit without
+// spilling (128 VGPRs at 16 wavefronts per workgroup): loaded rows x CPL <= 10.
+template <int DT, int R, bool GATE>
+hipError_t launch_group_r(int cpl, const WGroup& g, const float* x, hipStream_t s) {
+    constexpr int kRows = GATE ? 2 * R : R;
+    constexpr int kMaxCpl = kRows == 1 ? 8 : kRows == 2 ? 5 : 2;
     switch (cpl) {
-    case 1: return launch_stream_one<DT, R, 1, NW, FUSED>(w, a, x, y, s, probe, fits);
-    case 2: return launch_stream_one<DT, R, 2, NW, FUSED>(w, a, x, y, s, probe, fits);
+    case 1: return launch_group_one<DT, R, 1, GATE>(g, x, s);
+    case 2: return launch_group_one<DT, R, 2, GATE>(g, x, s);
     }
     if constexpr (kMaxCpl >= 5) {
         switch (cpl) {
-        case 3: return launch_stream_one<DT, R, 3, NW, FUSED>(w, a, x, y, s, probe, fits);
-        case 4: return launch_stream_one<DT, R, 4, NW, FUSED>(w, a, x, y, s, probe, fits);
-        case 5: return launch_stream_one<DT, R, 5, NW, FUSED>(w, a, x, y, s, probe, fits);
+        case 3: return launch_group_one<DT, R, 3, GATE>(g, x, s);
+        case 4: return launch_group_one<DT, R, 4, GATE>(g, x, s);
+        case 5: return launch_group_one<DT, R, 5, GATE>(g, x, s);
         }
     }
     if constexpr (kMaxCpl >= 8) {
         switch (cpl) {
-        case 6: return launch_stream_one<DT, R, 6, NW, FUSED>(w, a, x, y, s, probe, fits);
-        case 7: return launch_stream_one<DT, R, 7, NW, FUSED>(w, a, x, y, s, probe, fits);
-        default: return launch_stream_one<DT, R, 8, NW, FUSED>(w, a, x, y, s, probe, fits);
+        case 6: return launch_group_one<DT, R, 6, GATE>(g, x, s);
+        case 7: return launch_group_one<DT, R, 7, GATE>(g, x, s);
+        default: return launch_group_one<DT, R, 8, GATE>(g, x, s);
         }
     }
     return hipErrorInvalidValue;
 }
 
-// m == 1: chunks per lane cover the row in one pass up to K = 16384.  Rows
-// per wavefront: the fused kernel takes R = 2 once one 16-wavefront
-// workgroup per CU no longer covers the matrix with R = 1 (fewer workgroups
-// quantize the activation fewer times; R = 4 measured slower), the other the
-// smallest R in {1, 2} whose grid is resident at once.  XNQ_MV_STREAM_ROWS
-// forces R (tuning).
-template <int DT, bool FUSED>
-hipError_t launch_stream(const WView& w, const AView& a, const float* x, float* y, hipStream_t s) {
-    const uint32_t nchunks = w.k / 32;
+// m == 1 over a weight group: chunks per lane cover the row in one pass up
+// to K = 16384.  Rows per wavefront: R = 2 once one 16-wavefront workgroup
+// per CU no longer covers the loaded rows with R = 1 (fewer workgroups
+// quantize the activation fewer times; R = 4 measured slower), within the
+// register bound.  XNQ_MV_STREAM_ROWS=1|2 forces R (tuning).  Returns
+// hipErrorNotSupported for a GATE shape past the register bound.
+template <int DT, bool GATE>
+hipError_t launch_group(const WGroup& g, const float* x, hipStream_t s) {
+    const uint32_t nchunks = g.w[0].k / 32;
     const int cpl = (int)std::min<uint32_t>(8, (nchunks + 63) / 64);
+    if (GATE && cpl > 5) return hipErrorNotSupported;
     static const int forced = env_int("XNQ_MV_STREAM_ROWS", 0);
-    int r = forced;
-    if ((r == 2 && cpl > 5) || (r == 4 && cpl > 2)) r = 0;
-    if (r != 1 && r != 2 && (r != 4 || !FUSED)) {
-        if (FUSED) {  // R within the register bounds of launch_stream_r
-            int ncu = 1;
-            (void)wg_per_cu(reinterpret_cast<const void*>(stream_kernel<DT, 1, 1, 16, true>), 1024, 0, &ncu);
-            const uint32_t waves = (uint32_t)ncu * 16;
-            r = (w.n <= waves || cpl > 5) ? 1 : 2;  // R = 4 measured slower at 14336 rows
-        } else {
-            int fits = 0;
-            hipError_t e = launch_stream_r<DT, 1, FUSED>(cpl, w, a, x, y, s, true, &fits);
-            if (e != hipSuccess) return e;
-            r = fits ? 1 : 2;
-        }
-    }
-    if (r == 1) return launch_stream_r<DT, 1, FUSED>(cpl, w, a, x, y, s, false, nullptr);
-    if constexpr (FUSED) {
-        if (r == 4) return launch_stream_r<DT, 4, FUSED>(cpl, w, a, x, y, s, false, nullptr);
-    }
-    return launch_stream_r<DT, 2, FUSED>(cpl, w, a, x, y, s, false, nullptr);
+    int ncu = 1;
+    (void)wg_per_cu(reinterpret_cast<const void*>(group_kernel<DT, 1, 1, 16, false>), 1024, 0, &ncu);
+    const uint32_t waves = (uint32_t)ncu * 16;
+    const uint32_t loaded = GATE ? 2 * g.rows : g.rows;
+    int r = forced == 1 || forced == 2 ? forced : (loaded <= waves ? 1 : 2);
+    if (cpl > (GATE ? 2 : 5)) r = 1;
+    if (r == 1) return launch_group_r<DT, 1, GATE>(cpl, g, x, s);
+    return launch_group_r<DT, 2, GATE>(cpl, g, x, s);
 }
 
 inline int pick_cpl(uint32_t nchunks) {
@@ -612,7 +636,13 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
         hipError_t e;
         static const bool legacy = env_int("XNQ_MV_LEGACY", 0) != 0;
         if (mc == 1 && m == 1 && fused && !legacy) {
-            e = launch_stream<DT, true>(w, a, x, y, s);
+            WGroup g{};
+            g.w[0] = w;
+            g.y[0] = y;
+            g.row_end[0] = w.n;
+            g.count = 1;
+            g.rows = w.n;
+            e = launch_group<DT, false>(g, x, s);
         } else if (fused) {
             if (mc == 1) e = launch_cpl<DT, 1, true>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
             else if (mc == 2) e = launch_cpl<DT, 2, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
@@ -631,9 +661,18 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
 
 }  // namespace mv
 
+template <int DT>
+hipError_t launch_group_dt(const WGroup& g, const float* x, bool gate, hipStream_t s) {
+    return gate ? mv::launch_group<DT, true>(g, x, s) : mv::launch_group<DT, false>(g, x, s);
+}
+
 hipError_t launch_matvec_q4_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
 hipError_t launch_matvec_q8_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
 hipError_t launch_matvec_q4k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
 hipError_t launch_matvec_q6k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_group_q4_0(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q8_0(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q4k(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q6k(const WGroup&, const float*, bool, hipStream_t);
 
 }  // namespace xnq

@@ -8,4 +8,8 @@ hipError_t launch_matvec_q4_0(const WView& w, const AView& a, const float* x, si
     return mv::launch_dtype<XNQ_Q4_0>(w, a, x, m, y, s, fused);
 }
 
+hipError_t launch_group_q4_0(const WGroup& g, const float* x, bool gate, hipStream_t s) {
+    return launch_group_dt<XNQ_Q4_0>(g, x, gate, s);
+}
+
 }  // namespace xnq

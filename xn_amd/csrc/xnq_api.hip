@@ -471,6 +471,123 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     return st;
 }
 
+// ---------------------------------------------------------------------------
+// Decode-step groups: weights that read one activation row.
+
+// The grouped m == 1 kernel takes the group when every weight is on the
+// fused decode route with one dtype, one K and one device.
+static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m) {
+    if (m != 1 || count == 0 || count > (size_t)kMaxGroup) return false;
+    for (size_t i = 0; i < count; i++) {
+        if (!qts[i] || !fused_route(qts[i], m)) return false;
+        if (qts[i]->L.dtype != qts[0]->L.dtype || qts[i]->L.k != qts[0]->L.k || qts[i]->device != qts[0]->device)
+            return false;
+    }
+    return true;
+}
+
+static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* const* dsts) {
+    WGroup g{};
+    uint32_t end = 0;
+    for (size_t i = 0; i < count; i++) {
+        g.w[i] = make_wview(qts[i]->L, qts[i]->buf);
+        g.y[i] = dsts[i];
+        end += (uint32_t)qts[i]->L.n;
+        g.row_end[i] = end;
+    }
+    g.count = (uint32_t)count;
+    g.rows = end;
+    return g;
+}
+
+size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m) {
+    if (!gate || !up) return 0;
+    const xnq_qtensor* pair[2] = {gate, up};
+    if (group_route(pair, 2, m) && gate->L.k <= 64 * 5 * 32) return 0;
+    const size_t a = xnq_qtensor_matmul_t_workspace_size(gate, m), b = xnq_qtensor_matmul_t_workspace_size(up, m);
+    return align_up(a > b ? a : b, kAlign) + m * up->L.n * sizeof(float);
+}
+
+xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
+                                  const float* lhs_dev, void* workspace_dev, size_t workspace_bytes, float* dst_dev,
+                                  void* stream) {
+    xnq_status st = check_mkn(gate, m, k, n);
+    if (st) return st;
+    st = check_mkn(up, m, k, n);
+    if (st) return st;
+    if (gate->device != up->device) return fail(XNQ_ERR_INVALID, "gate and up live on different devices");
+    if (m == 0 || n == 0) return XNQ_OK;
+    if (!lhs_dev || !dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    const size_t need = xnq_matmul_t_silu_gate_workspace_size(gate, up, m);
+    hipStream_t s = (hipStream_t)stream;
+    if (need == 0) {
+        st = check_lhs(gate->L.dtype, k);
+        if (st) return st;
+        DeviceGuard g(gate->device);
+        if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+        const xnq_qtensor* pair[2] = {gate, up};
+        float* dsts[2] = {dst_dev, nullptr};
+        const WGroup grp = make_group(pair, 2, dsts);
+        WGroup gg = grp;
+        gg.rows = (uint32_t)n;
+        const hipError_t e = launch_matvec_group(gg, lhs_dev, true, s);
+        if (e != hipSuccess) return hip_fail(e, "silu-gated matvec kernel");
+        return XNQ_OK;
+    }
+    if (!workspace_dev || workspace_bytes < need)
+        return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
+    const size_t a = xnq_qtensor_matmul_t_workspace_size(gate, m), b = xnq_qtensor_matmul_t_workspace_size(up, m);
+    const size_t off = align_up(a > b ? a : b, kAlign);
+    float* u = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + off);
+    st = xnq_qtensor_matmul_t_ws(gate, m, k, n, lhs_dev, workspace_dev, off, dst_dev, stream);
+    if (!st) st = xnq_qtensor_matmul_t_ws(up, m, k, n, lhs_dev, workspace_dev, off, u, stream);
+    if (st) return st;
+    DeviceGuard g(gate->device);
+    const hipError_t e = launch_silu_mul(dst_dev, u, m * n, s);
+    if (e != hipSuccess) return hip_fail(e, "silu_mul kernel");
+    return XNQ_OK;
+}
+
+size_t xnq_matmul_t_group_workspace_size(const xnq_qtensor* const* qts, size_t count, size_t m) {
+    if (!qts || group_route(qts, count, m)) return 0;
+    size_t need = 0;
+    for (size_t i = 0; i < count; i++) {
+        const size_t b = qts[i] ? xnq_qtensor_matmul_t_workspace_size(qts[i], m) : 0;
+        if (b > need) need = b;
+    }
+    return need;
+}
+
+xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
+                              const float* lhs_dev, float* const* dsts_dev, void* workspace_dev,
+                              size_t workspace_bytes, void* stream) {
+    if (!qts || !dsts_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    for (size_t i = 0; i < count; i++) {
+        if (!qts[i]) return fail(XNQ_ERR_INVALID, "null qtensor");
+        const xnq_status st = check_mkn(qts[i], m, k, qts[i]->L.n);
+        if (st) return st;
+    }
+    if (count == 0 || m == 0) return XNQ_OK;
+    if (!lhs_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    for (size_t i = 0; i < count; i++)
+        if (!dsts_dev[i]) return fail(XNQ_ERR_INVALID, "null pointer");
+    if (group_route(qts, count, m)) {
+        const xnq_status st = check_lhs(qts[0]->L.dtype, k);
+        if (st) return st;
+        DeviceGuard g(qts[0]->device);
+        if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+        const hipError_t e = launch_matvec_group(make_group(qts, count, dsts_dev), lhs_dev, false, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "grouped matvec kernel");
+        return XNQ_OK;
+    }
+    for (size_t i = 0; i < count; i++) {
+        const xnq_status st = xnq_qtensor_matmul_t_ws(qts[i], m, k, qts[i]->L.n, lhs_dev, workspace_dev,
+                                                      workspace_bytes, dsts_dev[i], stream);
+        if (st) return st;
+    }
+    return XNQ_OK;
+}
+
 xnq_status xnq_qtensor_dequantize(const xnq_qtensor* qt, float* dst_dev, size_t elem_count,
                                   void* stream) {
     if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");

@@ -96,6 +96,19 @@ struct AView {
     ActImg A;
 };
 
+// Weights that share one activation row in a decode launch (matvec
+// kernels, m == 1): the row spaces of up to kMaxGroup weights of one dtype
+// and K laid end to end, each row's output to its own weight's destination;
+// or (gate) two weights of one shape combined as silu(x . w0) * (x . w1).
+constexpr int kMaxGroup = 3;
+struct WGroup {
+    WView w[kMaxGroup];
+    float* y[kMaxGroup];
+    uint32_t row_end[kMaxGroup];  // cumulative row counts
+    uint32_t count;
+    uint32_t rows;  // rows of the row space (gate: n)
+};
+
 bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string* err);
 ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k);
 uint32_t vec_dot_type(uint32_t weight_dtype);
@@ -146,6 +159,11 @@ hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float*
 hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hipStream_t s);
 // m == 1: quantizes the f32 row inside the kernel (no workspace).
 hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s);
+// m == 1 over a weight group (gate: silu(x . w0) * (x . w1)); hipErrorNotSupported
+// for a shape the grouped kernel does not take
+hipError_t launch_matvec_group(const WGroup& g, const float* x, bool gate, hipStream_t s);
+// g[i] = silu(g[i]) * u[i]
+hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t s);
 hipError_t launch_block_ints(const WView& w, const AView& a, size_t m,
                              int32_t* out, hipStream_t s);
 // k_mfma.hip

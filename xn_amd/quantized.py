@@ -369,6 +369,39 @@ Q4kHip = _backend_q("Q4kHip", GgmlDType.Q4K)
 Q6kHip = _backend_q("Q6kHip", GgmlDType.Q6K)
 
 
+# -- decode-step groups: weights that read one activation ----------------------
+
+def matmul_t_silu_gate(gate: QTensor, up: QTensor, mkn: Tuple[int, int, int], lhs: torch.Tensor,
+                       dst: torch.Tensor) -> None:
+    """dst = silu(lhs . gate^T) * (lhs . up^T): the SwiGLU of llama.rs:258-264
+    (silu(s) = s / (1 + exp(0 - s)), cpu_backend.rs:354-356); one kernel at
+    m = 1.  Runs on the current stream."""
+    m, k, n = gate._check_mm(mkn, lhs, dst)
+    L = _lib.load()
+    nbytes = L.xnq_matmul_t_silu_gate_workspace_size(gate.storage.handle, up.storage.handle, m)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gate.device) if nbytes else None
+    check(L.xnq_matmul_t_silu_gate(gate.storage.handle, up.storage.handle, m, k, n, _ptr(lhs),
+                                   _ptr(ws) if ws is not None else None, nbytes, _ptr(dst), _stream(gate.device)))
+
+
+def matmul_t_group(qts, m: int, k: int, lhs: torch.Tensor, dsts) -> None:
+    """dsts[i][m, n_i] = lhs . qts[i]^T for weights of one dtype and K (the q,
+    k, v projections of llama.rs:156-158); one kernel at m = 1."""
+    qts = list(qts)
+    dsts = list(dsts)
+    if len(qts) != len(dsts):
+        raise XnqError(1, f"{len(qts)} weights but {len(dsts)} destinations")
+    for qt, d in zip(qts, dsts):
+        qt._check_mm((m, k, qt.shape()[0]), lhs, d)
+    L = _lib.load()
+    hs = (ctypes.c_void_p * max(len(qts), 1))(*[qt.storage.handle for qt in qts])
+    ds = (ctypes.c_void_p * max(len(dsts), 1))(*[d.data_ptr() for d in dsts])
+    nbytes = L.xnq_matmul_t_group_workspace_size(hs, len(qts), m)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=lhs.device) if nbytes else None
+    check(L.xnq_matmul_t_group(hs, len(qts), m, k, _ptr(lhs), ds, _ptr(ws) if ws is not None else None, nbytes,
+                               _stream(lhs.device)))
+
+
 # -- lower-level entry points used by tests and the benchmark ------------------
 
 def set_route(route: int) -> None:
