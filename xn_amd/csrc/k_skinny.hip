@@ -1,24 +1,28 @@
 // Small-batch quantized matmul (m = 2 .. 64) on the int8 matrix cores.
 //
-// At a few rows the product is bound by the weight stream, so this kernel
-// keeps the weight path of a matvec (every weight byte read once, straight
-// from HBM into registers, no LDS) and does the dot products on
-// v_mfma_i32_32x32x32_i8: each wavefront owns 32 weight rows (output
-// columns) and all m activation rows (one or two 32-row MFMA tiles).  Per
-// super-block the wavefront expands its 32 columns' chunks into the two int8
-// digit planes of the prefill kernel (Q4K: sc = 8*sh + sl, digits sh*q and
-// sl*q; Q6K: sc*(q-32) = 128*hi + lo), contracts them against the activation
-// tile in LDS, and applies d_a * d_w in an f32 epilogue; the Q4K min term is
-// a K = 8 GEMM of -d_a*bsum32 by dmin*m_j on the bf16 matrix cores.  The
-// integer sums per super-block are exact, as in the reference's block dots
-// (k_quants.rs:1337-1416, 1743-1798).
+// At a few rows the product is bound by the weight stream, so every weight
+// byte is read once, and what limits the rate is how much of the stream is
+// in flight.  This kernel therefore fetches everything a super-block (256
+// columns of K) needs -- the weight chunks and block headers of its columns,
+// the activation tile in MFMA order, d_a and the Q8K block sums -- with
+// global_load_lds DMA into a ring of LDS slots two or three super-blocks
+// ahead of the one being multiplied, so the stream costs no registers and
+// the wavefronts do not wait on a load they issued just before.
 //
-// A workgroup (4 wavefronts, 128 columns) walks a range of super-blocks:
-// the next super-block's weights and activation tile are loaded into
-// registers while the current one is multiplied, and the activation tile is
-// written to the second LDS buffer after it.  When the column tiles alone do
-// not fill the GPU, the super-blocks are split across workgroups and the
+// A workgroup of 4 wavefronts owns 128 weight columns (output columns) and a
+// range of super-blocks; wavefront w owns columns 32w .. 32w+31 and all m
+// activation rows (one or two 32-row MFMA tiles).  Per super-block each
+// wavefront expands its columns' chunks from LDS into the two int8 digit
+// planes of the prefill kernel (Q4K: sc = 8*sh + sl, digits sh*q and sl*q;
+// Q6K: sc*(q-32) = 128*hi + lo), contracts them with the activation tile on
+// v_mfma_i32_32x32x32_i8 and applies d_a * d_w in an f32 epilogue; the Q4K
+// min term is a K = 8 GEMM of -d_a*bsum32 by dmin*m_j on the bf16 matrix
+// cores.  The integer sums per super-block are exact, as in the reference's
+// block dots (k_quants.rs:1337-1416, 1743-1798).  When the column tiles alone
+// do not fill the GPU, the super-blocks are split across workgroups and the
 // partial outputs are summed in split order afterwards.
+#include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "xnq_device.h"
@@ -36,22 +40,60 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4, kThreads = kWaves * 64, kCols = 32 * kWaves;
-
-// LDS image of one super-block of the activation rows (R = 32 * MT rows):
-//   q    [chunk 8][half 2][row R][16 bytes]   (MFMA A-operand order)
-//   min  Q4K: [row R][half 2][16 bytes] = bf16 hi4 | lo4 of -d_a * bsum32
-//        of sub-blocks 4*half .. 4*half+3
-//   d_a  [row R] f32
-template <int DT, int MT>
-struct SLay {
+// LDS slot of one super-block (byte offsets).  R = 32 * MT activation rows.
+//   wq   [col 128][slot 8][16]  weight chunk (slot ^ (col & 7)) of the column
+//   hdr  [wave 4][lane 64][16]  Q4K: d | dmin, scales[12]; Q6K: int8 scales[16]
+//                               of the wavefront's column lane & 31
+//   wh   Q6K [col 128][slot 4][16]  high-bit words of chunks 2p, 2p+1, p = slot ^ (col & 3)
+//   wd   Q6K [wave 4][lane 64] dword holding the f16 d of super-blocks 2j, 2j+1
+//   act  [chunk 8][half 2][row R][16]  activation quants in MFMA A order
+//   bs   Q4K [row R][part 2][16]   chunk bsum pairs of sub-blocks 4*part .. +3
+//   da   [64] f32 d_a per row (rows past m repeat the last)
+// The XOR slot order makes the 32 columns' reads of one chunk hit distinct
+// banks while each column's bytes still arrive as one 128-byte line.
+template <int DT, int MT, int NW>
+struct KLay {
+    static constexpr bool kQ4K = DT == XNQ_Q4K;
+    static constexpr int kWaves = NW, kThreads = 64 * NW, kCols = 32 * NW;
     static constexpr int R = 32 * MT;
-    static constexpr int kQ = 256 * R;
-    static constexpr int kMin = DT == XNQ_Q4K ? 32 * R : 0;
-    static constexpr int kBuf = kQ + kMin + 4 * R;
-    static constexpr int kLds = 2 * kBuf;
-    static constexpr int kPieces = 16 * R / kThreads;  // 16-byte activation pieces per thread
+    static constexpr int kWq = 0;
+    static constexpr int kHdr = kWq + kCols * 128;
+    static constexpr int kWh = kHdr + kWaves * 64 * 16;
+    static constexpr int kWd = kWh + (kQ4K ? 0 : kCols * 64);
+    static constexpr int kAct = kWd + (kQ4K ? 0 : kWaves * 64 * 4);
+    static constexpr int kBs = kAct + 8 * 2 * R * 16;
+    static constexpr int kDa = kBs + (kQ4K ? R * 32 : 0);
+    static constexpr int kDummy = kDa + 64 * 4;  // target of the padding DMA
+    static constexpr int kSlot = kDummy + 64 * 4;
+    static constexpr int kRing = (4 * kSlot <= 160 * 1024) ? 4 : (3 * kSlot <= 160 * 1024) ? 3 : 2;
+    static constexpr int kLds = kRing * kSlot;
+    // DMA instructions per wavefront per super-block, the same in every
+    // wavefront so one vmcnt count fits all: weights, activation pieces, and
+    // one of {bsums, d_a, padding}
+    static constexpr int kActPer = 8 * MT / NW;  // 8 * MT KiB of activation over NW wavefronts
+    static constexpr int kWPer = kQ4K ? 4 + 1 : 4 + 1 + 2 + 1;
+    static constexpr int kD = kWPer + kActPer + 1;
+    static_assert(kLds <= 160 * 1024, "LDS budget");
+    static_assert(2 * kD < 64, "vmcnt range");
 };
+
+// global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
+// holds the LDS address lane 0 writes (lane i writes i * size beyond it).
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds_addr)),
+                 "v"(off), "s"(base)
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds_addr)),
+                 "v"(off), "s"(base)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // bytes of d (each <= 15) times s (<= 7): one packed 16-bit multiply
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
@@ -86,184 +128,125 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
     return make_uint4(hu.x, hu.y, lu.x, lu.y);
 }
 
-typedef unsigned int nt_u4 __attribute__((ext_vector_type(4)));
-
-// weight stream: read once per call, non-temporal
-__device__ __forceinline__ uint4 ldw(const uint4* p) {
-    const nt_u4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u4*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// One super-block of this lane's weight column, in registers.  Lanes 0-31
-// load chunks 0-3 (Q6K: high-bit words 0-1) of their column and lanes 32-63
-// chunks 4-7 (words 2-3) of the same column, so each load instruction
-// touches 32 rows once instead of twice; one v_permlane32_swap per dword
-// then gives every lane all of them.
-template <int DT>
-struct WeightSB {
-    uint4 q[4];   // raw: this half's four chunks
-    uint4 s;      // Q4K: d | dmin, scales[12]; Q6K: int8 scales[16]
-    uint4 h[2];   // Q6K: this half's high-bit words
-    uint32_t d;   // Q6K: f16 d
-};
-
-template <int DT>
-__device__ __forceinline__ void load_weight_sb(const WView& w, uint32_t col, uint32_t sb, WeightSB<DT>& x) {
-    const uint32_t hsel = (threadIdx.x & 63) >> 5;
-    const uint4* q = reinterpret_cast<const uint4*>(w.q + col * w.q_row + sb * 128) + 4 * hsel;
-#pragma unroll
-    for (int c = 0; c < 4; c++) x.q[c] = ldw(&q[c]);
-    x.s = *reinterpret_cast<const uint4*>(w.s + col * w.s_row + sb * 16);
-    if (DT == XNQ_Q6K) {
-        const uint4* h = reinterpret_cast<const uint4*>(w.h + col * w.h_row + sb * 64) + 2 * hsel;
-#pragma unroll
-        for (int i = 0; i < 2; i++) x.h[i] = ldw(&h[i]);
-        x.d = *reinterpret_cast<const uint16_t*>(w.d + col * w.d_row + sb * 2);
-    }
-}
-
-// (lanes 0-31 value, lanes 32-63 value) -> lo = the lanes-0-31 value, hi = the lanes-32-63 value, in every lane
-__device__ __forceinline__ void join_halves(uint32_t v, uint32_t& lo, uint32_t& hi) {
-    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    lo = r[0];
-    hi = r[1];
-}
-__device__ __forceinline__ void join_halves4(uint4 v, uint4& lo, uint4& hi) {
-    join_halves(v.x, lo.x, hi.x);
-    join_halves(v.y, lo.y, hi.y);
-    join_halves(v.z, lo.z, hi.z);
-    join_halves(v.w, lo.w, hi.w);
-}
-
-// Activation pieces of one super-block, in registers on their way to LDS
-// (named members, not an array, so that they stay in registers).
-template <int DT, int MT>
-struct ActSB {
-    uint4 q0, q1, q2, q3;  // pieces t, t + 256, (MT == 2) t + 512, t + 768
-    int4 sums;             // Q4K: chunk bsum pairs of sub-blocks 4*half .. (threads < 2R)
-    float da;              // d_a of the thread's row (threads < 2R)
-};
-
-// Piece p of a super-block's activation tile: chunk fastest, so 8
-// consecutive threads read one row's 128 contiguous bytes of a half.
-template <int DT, int MT>
-__device__ __forceinline__ uint4 load_piece(const AView& a, uint32_t m, uint32_t sb, uint32_t p) {
-    const uint32_t c = p & 7, half = (p >> 3) & 1, row = min(p >> 4, m - 1);
-    return *reinterpret_cast<const uint4*>(a.img + row * a.A.row_bytes + half * (a.A.k / 2) + (sb * 8 + c) * 16);
-}
-
-template <int DT, int MT>
-__device__ __forceinline__ void store_piece(uint8_t* buf, uint32_t p, uint4 v) {
-    using L = SLay<DT, MT>;
-    const uint32_t c = p & 7, half = (p >> 3) & 1, row = p >> 4;
-    *reinterpret_cast<uint4*>(buf + ((c * 2 + half) * L::R + row) * 16) = v;
-}
-
-template <int DT, int MT>
-__device__ __forceinline__ void load_act_sb(const AView& a, uint32_t m, uint32_t sb, ActSB<DT, MT>& x) {
-    using L = SLay<DT, MT>;
-    static_assert(L::kPieces == 2 || L::kPieces == 4, "pieces per thread");
-    const uint32_t t = threadIdx.x;
-    const ActImg& A = a.A;
-    x.q0 = load_piece<DT, MT>(a, m, sb, t);
-    x.q1 = load_piece<DT, MT>(a, m, sb, t + kThreads);
-    if (L::kPieces == 4) {
-        x.q2 = load_piece<DT, MT>(a, m, sb, t + 2 * kThreads);
-        x.q3 = load_piece<DT, MT>(a, m, sb, t + 3 * kThreads);
-    }
-    x.da = 0.0f;
-    x.sums = make_int4(0, 0, 0, 0);
-    if (t < 2 * L::R) {
-        const uint32_t row = min(t >> 1, m - 1);
-        x.da = reinterpret_cast<const float*>(a.img + row * A.row_bytes + A.d_off)[sb];
-        if (DT == XNQ_Q4K)
-            x.sums = *reinterpret_cast<const int4*>(a.img + row * A.row_bytes + A.s_off + sb * 32 + (t & 1) * 16);
-    }
-}
-
-template <int DT, int MT>
-__device__ __forceinline__ void store_act_sb(const ActSB<DT, MT>& x, uint8_t* buf) {
-    using L = SLay<DT, MT>;
-    const uint32_t t = threadIdx.x;
-    store_piece<DT, MT>(buf, t, x.q0);
-    store_piece<DT, MT>(buf, t + kThreads, x.q1);
-    if (L::kPieces == 4) {
-        store_piece<DT, MT>(buf, t + 2 * kThreads, x.q2);
-        store_piece<DT, MT>(buf, t + 3 * kThreads, x.q3);
-    }
-    if (t < 2 * L::R) {
-        const uint32_t row = t >> 1, half = t & 1;
-        if (half == 0) reinterpret_cast<float*>(buf + L::kQ + L::kMin)[row] = x.da;
-        if (DT == XNQ_Q4K) {
-            const int32_t prs[4] = {x.sums.x, x.sums.y, x.sums.z, x.sums.w};
-            float v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                v[u] = -x.da * (float)((int)(int16_t)(prs[u] & 0xffff) + (int)(int16_t)(prs[u] >> 16));
-            *reinterpret_cast<uint4*>(buf + L::kQ + (row * 2 + half) * 16) = bf16_split4(v);
-        }
-    }
-}
-
-template <int DT, int MT>
-__global__ __launch_bounds__(kThreads) void skinny_kernel(WView w, AView a, uint32_t m, uint32_t sb_per_split,
+template <int DT, int MT, int NW>
+__global__ __launch_bounds__(64 * NW) void skinny_kernel(WView w, AView a, uint32_t m, uint32_t sb_per_split,
                                                           float* __restrict__ y, size_t split_stride) {
-    using L = SLay<DT, MT>;
-    constexpr bool kQ4K = DT == XNQ_Q4K;
+    using L = KLay<DT, MT, NW>;
+    constexpr int kCols = L::kCols;
+    constexpr bool kQ4K = L::kQ4K;
     constexpr int kShift = kQ4K ? 3 : 7;
+    constexpr int kD = L::kD;
+    constexpr int kRing = L::kRing;
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lrow = lane & 31, half = lane >> 5;
     const uint32_t sb0 = blockIdx.y * sb_per_split;
     const uint32_t nsb = min(sb_per_split, w.k / 256 - sb0);
     y += blockIdx.y * split_stride;
-    const uint32_t ncol = blockIdx.x * kCols + wave * 32 + lrow;  // this lane's output column
-    const uint32_t col = min(ncol, w.n - 1);
+    const uint32_t col0 = blockIdx.x * kCols;
+    const uint32_t ncol = col0 + wave * 32 + lrow;  // this lane's output column
+    const uint32_t lbase = (uint32_t)(uintptr_t)lds;  // low half of the flat address = LDS offset
+    const ActImg& A = a.A;
+    // lanes past the last column or row re-read the last one (every DMA
+    // instruction is issued by the whole wavefront: vmcnt counts instructions);
+    // those outputs are dropped at the store
+    const uint32_t cmax = w.n - 1, rmax = m - 1;
+    // Q4K: bsums take the first MT wavefronts' extra instruction, d_a the next
+    constexpr uint32_t kExtraBs = kQ4K ? (uint32_t)MT : 0u;
+
+    // ---- the DMA of super-block i: kD instructions per wavefront ----
+    // Per-lane byte offsets are fixed for the whole walk; the super-block
+    // moves only the uniform base pointers.
+    // weight chunks: instruction j covers columns 32*wave + 8j .. +7,
+    // lane = 8 * column + slot, slot s holding chunk s ^ (column & 7)
+    uint32_t oq[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t cl = wave * 32 + 8 * j + (lane >> 3);
+        oq[j] = min(col0 + cl, cmax) * w.q_row + ((lane & 7) ^ (cl & 7)) * 16;
+    }
+    // block header (Q4K) / scales (Q6K) of column lane & 31; Q6K d dword
+    const uint32_t ocol = min(col0 + wave * 32 + lrow, cmax);
+    const uint32_t os = ocol * w.s_row, od = ocol * w.d_row;
+    // Q6K high-bit words: instruction j covers columns 32*wave + 16j .. +15,
+    // lane = 4 * column + slot, slot s holding chunk pair s ^ (column & 3)
+    uint32_t oh[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t cl = wave * 32 + 16 * j + (lane >> 2);
+        oh[j] = kQ4K ? 0u : min(col0 + cl, cmax) * w.h_row + ((lane & 3) ^ (cl & 3)) * 16;
+    }
+    // activation pieces of 1 KiB.  MT == 1: piece = chunk c, lanes 0-31 rows
+    // of half 0, lanes 32-63 rows of half 1.  MT == 2: piece = (chunk, half),
+    // lane = row.
+    uint32_t oa[L::kActPer];
+#pragma unroll
+    for (int j = 0; j < L::kActPer; j++) {
+        const uint32_t t = wave * L::kActPer + j;
+        const uint32_t c = MT == 1 ? t : t >> 1;
+        const uint32_t hsel = MT == 1 ? half : (t & 1);
+        const uint32_t row = MT == 1 ? lrow : lane;
+        oa[j] = min(row, rmax) * A.row_bytes + hsel * (A.k / 2) + c * 16;
+    }
+    // the extra instruction: Q4K bsums (rows 32*wave .. +31), d_a, or padding
+    const uint32_t obs = min(wave * 32 + (lane >> 1), rmax) * A.row_bytes + A.s_off + (lane & 1) * 16;
+    const uint32_t oda = min(lane, rmax) * A.row_bytes + A.d_off;
+
+    auto issue = [&](uint32_t i) {
+        const uint32_t sb = sb0 + i;
+        const uint32_t slot = lbase + (i % kRing) * L::kSlot;
+#pragma unroll
+        for (int j = 0; j < 4; j++) dma16(w.q + sb * 128, oq[j], slot + L::kWq + (wave * 32 + 8 * j) * 128);
+        dma16(w.s + sb * 16, os, slot + L::kHdr + wave * 64 * 16);
+        if (!kQ4K) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + (wave * 32 + 16 * j) * 64);
+            dma4(w.d + (sb & ~1u) * 2, od, slot + L::kWd + wave * 64 * 4);
+        }
+#pragma unroll
+        for (int j = 0; j < L::kActPer; j++) {
+            const uint32_t t = wave * L::kActPer + j;
+            const uint32_t c = MT == 1 ? t : t >> 1;
+            const uint32_t hsel = MT == 1 ? 0u : (t & 1);
+            dma16(a.img + sb * 128, oa[j], slot + L::kAct + (c * 2 + hsel) * L::R * 16);
+        }
+        if (wave < kExtraBs) dma16(a.img + sb * 32, obs, slot + L::kBs + wave * 32 * 32);
+        else if (wave == kExtraBs) dma4(a.img + sb * 4, oda, slot + L::kDa);
+        else dma4(a.img + sb * 4, oda, slot + L::kDummy);
+    };
 
     v16f acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[t] = v16f{};
 
-    WeightSB<DT> wa, wb;  // two weight buffers, alternated statically (no register copies)
-    load_weight_sb<DT>(w, col, sb0, wa);
-    {
-        ActSB<DT, MT> a0;
-        load_act_sb<DT, MT>(a, m, sb0, a0);
-        store_act_sb<DT, MT>(a0, lds);
-    }
-    __syncthreads();
-
-    // super-block i from `wcur`; super-block i+1 is fetched into `wnext`
-    auto step = [&](uint32_t i, WeightSB<DT>& wcur, WeightSB<DT>& wnext) __attribute__((always_inline)) {
-        const uint32_t sb = sb0 + i;
-        const bool more = i + 1 < nsb;
-        ActSB<DT, MT> anext;
-        if (more) {
-            // activation first: its LDS store below then waits only for these
-            // loads, not for the weight loads, which stay in flight until the
-            // next super-block
-            load_act_sb<DT, MT>(a, m, sb + 1, anext);
-            __builtin_amdgcn_sched_barrier(0);  // keep every activation load ahead of the weight loads
-            load_weight_sb<DT>(w, col, sb + 1, wnext);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        const uint8_t* buf = lds + (i & 1) * L::kBuf;
-        uint4 qc[8], hq[4];
+    // prologue: super-blocks 0 .. kRing-2 in flight
 #pragma unroll
-        for (int c = 0; c < 4; c++) join_halves4(wcur.q[c], qc[c], qc[c + 4]);
-        if (!kQ4K) {
-            join_halves4(wcur.h[0], hq[0], hq[2]);
-            join_halves4(wcur.h[1], hq[1], hq[3]);
-        }
+    for (int i = 0; i < kRing - 1; i++)
+        if ((uint32_t)i < nsb) issue(i);
+
+    for (uint32_t i = 0; i < nsb; i++) {
+        // wait for super-block i: the younger ones in flight are i+1 .. i+kRing-2
+        const uint32_t younger = min((uint32_t)(kRing - 2), nsb - 1 - i);
+        if (kRing >= 4 && younger >= 2) wait_vm<2 * kD>();
+        else if (kRing >= 3 && younger >= 1) wait_vm<kD>();
+        else wait_vm<0>();
+        __syncthreads();  // every wavefront's DMA of i landed; slot (i-1) % kRing is free
+        if (i + kRing - 1 < nsb) issue(i + kRing - 1);
+
+        const uint8_t* S = lds + (i % kRing) * L::kSlot;
+        const uint32_t cl = wave * 32 + lrow;
+        const uint4 hdr = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 64 + lrow) * 16);
         v16i hi[MT], lo[MT];
 #pragma unroll
         for (int c = 0; c < 8; c++) {
+            const uint4 qc = *reinterpret_cast<const uint4*>(S + L::kWq + cl * 128 + ((c ^ (cl & 7)) * 16));
             uint32_t p0[4], p1[4];  // high and low digit of this lane's 16 elements of chunk c
             if (kQ4K) {
                 int sc, mn;
-                q4k_scale_min(wcur.s.y, wcur.s.z, wcur.s.w, c, sc, mn);
+                q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc, mn);
                 const uint32_t sh = (uint32_t)sc >> 3, sl = (uint32_t)sc & 7;
-                const uint32_t q4[4] = {qc[c].x, qc[c].y, qc[c].z, qc[c].w};
+                const uint32_t q4[4] = {qc.x, qc.y, qc.z, qc.w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const uint32_t nib = (q4[j] >> (4 * half)) & 0x0F0F0F0Fu;
@@ -271,11 +254,11 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(WView w, AView a, uint
                     p1[j] = mul_bytes(nib, sl);
                 }
             } else {
-                const uint4 hw = hq[c >> 1];
-                const uint2 qh = (c & 1) ? make_uint2(hw.z, hw.w) : make_uint2(hw.x, hw.y);
+                const uint2 qh = *reinterpret_cast<const uint2*>(S + L::kWh + cl * 64 + (((c >> 1) ^ (cl & 3)) * 16) +
+                                                                 (c & 1) * 8);
                 int b[8];
-                q6k_unpack(qc[c], qh, b);
-                const uint32_t sw = (c >> 1) == 0 ? wcur.s.x : (c >> 1) == 1 ? wcur.s.y : (c >> 1) == 2 ? wcur.s.z : wcur.s.w;
+                q6k_unpack(qc, qh, b);
+                const uint32_t sw = (c >> 1) == 0 ? hdr.x : (c >> 1) == 1 ? hdr.y : (c >> 1) == 2 ? hdr.z : hdr.w;
                 const int sc = (int)(int8_t)(sw >> (8 * (2 * (c & 1) + half)));
 #pragma unroll
                 for (int j = 0; j < 4; j++) q6_digits((uint32_t)b[4 * half + j], sc, p1[j], p0[j]);
@@ -284,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(WView w, AView a, uint
             const v4i b1 = {(int)p1[0], (int)p1[1], (int)p1[2], (int)p1[3]};
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const v4i av = *reinterpret_cast<const v4i*>(buf + ((c * 2 + half) * L::R + t * 32 + lrow) * 16);
+                const v4i av = *reinterpret_cast<const v4i*>(S + L::kAct + ((c * 2 + half) * L::R + t * 32 + lrow) * 16);
                 if (c == 0) {
                     hi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, v16i{}, 0, 0, 0);
                     lo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, v16i{}, 0, 0, 0);
@@ -295,16 +278,22 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(WView w, AView a, uint
             }
         }
         // epilogue: acc += d_a d_w (hi * 2^s + lo)  [- d_a dmin sum_j m_j bsum32_j]
-        const float* eda = reinterpret_cast<const float*>(buf + L::kQ + L::kMin);
-        const float dw = f16_bits_to_f32(kQ4K ? (wcur.s.x & 0xffffu) : wcur.d);
+        const float* eda = reinterpret_cast<const float*>(S + L::kDa);
+        float dw;
+        if (kQ4K) {
+            dw = f16_bits_to_f32(hdr.x & 0xffffu);
+        } else {
+            const uint32_t dd = reinterpret_cast<const uint32_t*>(S + L::kWd)[wave * 64 + lrow];
+            dw = f16_bits_to_f32(((sb0 + i) & 1) ? (dd >> 16) : (dd & 0xffffu));
+        }
         v8bf bh8, bl8;
         if (kQ4K) {
-            const float dm = f16_bits_to_f32(wcur.s.x >> 16);
+            const float dm = f16_bits_to_f32(hdr.x >> 16);
             float v[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 int sc2, mn2;
-                q4k_scale_min(wcur.s.y, wcur.s.z, wcur.s.w, (int)(4 * half + u), sc2, mn2);
+                q4k_scale_min(hdr.y, hdr.z, hdr.w, (int)(4 * half + u), sc2, mn2);
                 v[u] = dm * (float)mn2;
             }
             const uint4 bv = bf16_split4(v);
@@ -324,19 +313,20 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(WView w, AView a, uint
                 }
             }
             if (kQ4K) {
-                const uint4 av = *reinterpret_cast<const uint4*>(buf + L::kQ + ((t * 32 + lrow) * 2 + half) * 16);
-                const v8bf a8 = __builtin_bit_cast(v8bf, av);
+                // row side of the min term: -d_a * bsum32 of sub-blocks 4*half .. +3
+                const uint32_t row = t * 32 + lrow;
+                const uint4 pr = *reinterpret_cast<const uint4*>(S + L::kBs + (row * 2 + half) * 16);
+                const float da = eda[row];
+                const uint32_t prs[4] = {pr.x, pr.y, pr.z, pr.w};
+                float v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    v[u] = -da * (float)((int)(int16_t)(prs[u] & 0xffffu) + (int)(int16_t)(prs[u] >> 16));
+                const v8bf a8 = __builtin_bit_cast(v8bf, bf16_split4(v));
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bh8, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bl8, acc[t], 0, 0, 0);
             }
         }
-        if (more) store_act_sb<DT, MT>(anext, lds + ((i + 1) & 1) * L::kBuf);
-        __syncthreads();
-    };
-    for (uint32_t i = 0; i < nsb; i += 2) {
-        step(i, wa, wb);
-        if (i + 1 >= nsb) break;
-        step(i + 1, wb, wa);
     }
 
     if (ncol < w.n) {
@@ -350,16 +340,24 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(WView w, AView a, uint
     }
 }
 
-template <int DT, int MT>
+template <int DT, int MT, int NW>
 hipError_t launch_skinny_dt(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                             hipStream_t s) {
-    using L = SLay<DT, MT>;
+    using L = KLay<DT, MT, NW>;
+    constexpr int kCols = L::kCols;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(skinny_kernel<DT, MT, NW>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
     const uint32_t nsb = w.k / 256;
     const uint32_t per = (nsb + splits - 1) / splits;
-    splits = (nsb + per - 1) / per;
+    splits = (nsb + per - 1) / per;  // every split non-empty
     const dim3 grid((w.n + kCols - 1) / kCols, splits);
     float* out = splits > 1 ? partial : y;
-    hipLaunchKernelGGL((skinny_kernel<DT, MT>), grid, dim3(kThreads), L::kLds, s, w, a, (uint32_t)m, per, out,
+    hipLaunchKernelGGL((skinny_kernel<DT, MT, NW>), grid, dim3(L::kThreads), L::kLds, s, w, a, (uint32_t)m, per, out,
                        splits > 1 ? m * (size_t)w.n : (size_t)0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
@@ -368,13 +366,29 @@ hipError_t launch_skinny_dt(const WView& w, const AView& a, size_t m, uint32_t s
 
 }  // namespace
 
+// Wavefronts per workgroup (32 columns each): 8 (two per SIMD, so one
+// wavefront's expansion overlaps the other's waits) where the column tiles
+// still cover the CUs with K split at most 4 ways, else 4.  XNQ_SKINNY_NW=4|8
+// forces it (tuning).
+static int skinny_waves(size_t n, size_t k) {
+    static const int forced = [] {
+        const char* e = getenv("XNQ_SKINNY_NW");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced == 4 || forced == 8) return forced;
+    const size_t tiles8 = (n + 255) / 256, nsb = k / 256;
+    return tiles8 * std::min<size_t>(4, nsb / 2) >= 200 ? 8 : 4;
+}
+
 uint32_t skinny_splits(size_t m, size_t n, size_t k) {
     (void)m;
-    // about three workgroups per CU, at least one super-block per split
-    const size_t tiles = (n + kCols - 1) / kCols;
+    // the LDS ring takes most of a CU, so one workgroup per CU: split K while
+    // the grid still fits the 256 CUs at once, each split at least two
+    // super-blocks long
+    const size_t tiles = (n + 32 * skinny_waves(n, k) - 1) / (32 * skinny_waves(n, k));
     const size_t nsb = k / 256;
-    size_t splits = (768 + tiles - 1) / tiles;
-    if (splits > nsb) splits = nsb;
+    size_t splits = 256 / tiles;
+    if (splits > nsb / 2) splits = nsb / 2;
     return splits < 1 ? 1u : (uint32_t)splits;
 }
 
@@ -388,12 +402,18 @@ hipError_t launch_skinny(const WView& w, const AView& a, size_t m, uint32_t spli
     if (m == 0 || w.n == 0) return hipSuccess;
     if (m > 64) return hipErrorInvalidValue;
     if (splits > 1 && !partial) splits = 1;
-    if (w.dtype == XNQ_Q4K)
-        return m <= 32 ? launch_skinny_dt<XNQ_Q4K, 1>(w, a, m, splits, y, partial, s)
-                       : launch_skinny_dt<XNQ_Q4K, 2>(w, a, m, splits, y, partial, s);
-    if (w.dtype == XNQ_Q6K)
-        return m <= 32 ? launch_skinny_dt<XNQ_Q6K, 1>(w, a, m, splits, y, partial, s)
-                       : launch_skinny_dt<XNQ_Q6K, 2>(w, a, m, splits, y, partial, s);
+    const bool w8 = skinny_waves(w.n, w.k) == 8;
+#define XNQ_SK(DT)                                                                                   \
+    if (w.dtype == DT) {                                                                             \
+        if (m <= 32)                                                                                 \
+            return w8 ? launch_skinny_dt<DT, 1, 8>(w, a, m, splits, y, partial, s)                  \
+                      : launch_skinny_dt<DT, 1, 4>(w, a, m, splits, y, partial, s);                 \
+        return w8 ? launch_skinny_dt<DT, 2, 8>(w, a, m, splits, y, partial, s)                      \
+                  : launch_skinny_dt<DT, 2, 4>(w, a, m, splits, y, partial, s);                     \
+    }
+    XNQ_SK(XNQ_Q4K)
+    XNQ_SK(XNQ_Q6K)
+#undef XNQ_SK
     return hipErrorNotSupported;
 }
 

@@ -338,7 +338,8 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
 }
 
 // Automatic routes (measured on MI355X):
-//   m < 12 (m < 8 when k >= 8192)   matvec kernels (up to 8 rows per launch)
+//   m < 12 (m < 8 when k >= 8192,
+//   m < 6 for Q4K with n >= 8192)   matvec kernels (up to 8 rows per launch)
 //   m <= 64                          skinny int8-MFMA kernel for Q4K / Q6K
 //   larger m                         tiled int8-MFMA prefill kernel
 // Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MAX_ROWS and
@@ -357,7 +358,10 @@ static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k) {
     if (forced == 1) return kMatvec;
     if (forced == 2) return kMfma;
     if (forced == 3) return kSkinny;
-    const size_t skinny_lo = skinny_min ? skinny_min : (k >= 8192 ? 8 : 12);
+    // measured crossovers: the matvec kernels' cost grows with every row, the
+    // skinny kernel's hardly at all below 32 rows
+    const size_t skinny_lo =
+        skinny_min ? skinny_min : (dtype == XNQ_Q4K && n >= 8192) ? 6 : (k >= 8192 ? 8 : 12);
     if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
     if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
     return kMatvec;
