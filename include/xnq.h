@@ -184,6 +184,22 @@ xnq_status xnq_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const
 xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* workspace_dev,
                                   int32_t* out_dev, void* stream);
 
+/* Stream capture into a replayable graph (xn's Device::capture_begin /
+ * capture_end / CaptureGraph::launch, cuda_backend/mod.rs:251-283): every
+ * launch the library makes on `stream` between begin and end is recorded,
+ * not run; xnq_graph_launch replays it with the same device pointers.  Inside
+ * a capture use the entry points that allocate nothing: matmul_t_ws,
+ * quantize_lhs + matmul_preq, silu_gate / group with their workspaces, and
+ * matmul_t on the decode route (m <= 8); matmul_t fails with XNQ_ERR_INVALID
+ * where it would allocate.  A failed capture is discarded with
+ * xnq_capture_abort. */
+typedef struct xnq_graph xnq_graph;
+xnq_status xnq_capture_begin(void* stream);
+xnq_status xnq_capture_end(void* stream, xnq_graph** out);
+void xnq_capture_abort(void* stream);
+xnq_status xnq_graph_launch(const xnq_graph* g, void* stream);
+void xnq_graph_free(xnq_graph* g);
+
 #ifdef __cplusplus
 }
 #endif

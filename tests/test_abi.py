@@ -44,7 +44,7 @@ def test_sizes_match_ggml(lib):
         if lib.xnq_type_size(int(dt)):
             assert lib.xnq_type_size(int(dt)) == dt.type_size()
             assert lib.xnq_block_size(int(dt)) == dt.block_size()
-    assert lib.xnq_abi_version() == 3
+    assert lib.xnq_abi_version() == 4
 
 
 def test_host_validation(lib):
@@ -72,3 +72,10 @@ def test_product_does_not_import_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.lower(), os.path.join(dirpath, f)
+
+
+def test_capture_needs_a_stream(lib):
+    # the null stream cannot be captured (cuda_backend/mod.rs:264 captures the device stream)
+    assert lib.xnq_capture_begin(None) == 1
+    assert b"null stream" in lib.xnq_last_error()
+    assert lib.xnq_graph_launch(None, None) == 1

@@ -308,3 +308,78 @@ def test_matmul_group_mixed_dtypes(orc, dev):
     matmul_t_group(qts, 1, k, torch.from_numpy(x).to(dev), dsts)
     for d, b, (dt, n) in zip(dsts, blocks, specs):
         assert_close(d.cpu().numpy(), orc.matmul(dt, x, b, n), f"mixed group dt={dt}")
+
+
+# ------------------------------------------------ stream capture
+def test_capture_graph_replay(orc, dev):
+    """Launches captured with xnq_capture_begin/end (Device::capture_begin /
+    capture_end, cuda_backend/mod.rs:251-283) replay to the eager results,
+    on every replay, with eager work and new inputs between replays."""
+    from xn_amd.quantized import capture, matmul_t_silu_gate
+
+    rng = np.random.default_rng(8400)
+    k, n = 1024, 256
+    b4 = orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)))
+    bg = orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)))
+    bu = orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)))
+    b6 = orc.from_float(Q6K, rng.normal(0, 0.02, (n, k)))
+    q4, g, u, q6 = (upload(b, n, k, dt, dev) for b, dt in ((b4, Q4K), (bg, Q4K), (bu, Q4K), (b6, Q6K)))
+    xs = {m: torch.zeros((m, k), dtype=torch.float32, device=dev) for m in (1, 16, 300)}
+    ys = {name: torch.zeros((m, n), dtype=torch.float32, device=dev)
+          for name, m in (("mv", 1), ("gate", 1), ("sk", 16), ("mf", 300))}
+    ws16 = torch.empty(max(q6.matmul_t_workspace_size(16), 1), dtype=torch.uint8, device=dev)
+    ws300 = torch.empty(max(q4.matmul_t_workspace_size(300), 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream(dev)
+
+    def run():
+        q4.matmul_t((1, k, n), xs[1], ys["mv"])
+        matmul_t_silu_gate(g, u, (1, k, n), xs[1], ys["gate"])
+        q6.matmul_t_ws((16, k, n), xs[16], ws16, ys["sk"])
+        q4.matmul_t_ws((300, k, n), xs[300], ws300, ys["mf"])
+
+    torch.cuda.synchronize()
+    with capture(stream) as c:
+        run()
+    assert c.graph is not None
+    for rep in range(3):
+        host = {m: rng.normal(0, 1, (m, k)).astype(np.float32) for m in xs}
+        with torch.cuda.stream(stream):
+            for m in xs:
+                xs[m].copy_(torch.from_numpy(host[m]))
+            for y in ys.values():
+                y.fill_(float("nan"))
+        stream.synchronize()
+        c.graph.launch(stream)
+        stream.synchronize()
+        got = {name: y.clone() for name, y in ys.items()}
+        with torch.cuda.stream(stream):
+            for y in ys.values():
+                y.fill_(float("nan"))
+            run()
+        stream.synchronize()
+        for name, y in ys.items():
+            assert torch.equal(got[name], y), f"replay {rep}: {name} differs from the eager result"
+        if rep == 0:
+            assert_close(got["mv"].cpu().numpy(), orc.matmul(Q4K, host[1], b4, n), "captured matvec")
+            assert_close(got["sk"].cpu().numpy(), orc.matmul(Q6K, host[16], b6, n), "captured skinny")
+            assert_close(got["mf"].cpu().numpy(), orc.matmul(Q4K, host[300], b4, n), "captured prefill")
+
+
+def test_matmul_t_refuses_to_allocate_in_capture(orc, dev):
+    from xn_amd._lib import XnqError
+    from xn_amd.quantized import capture
+
+    rng = np.random.default_rng(8500)
+    k, n = 1024, 64
+    qt = upload(orc.from_float(Q4K, rng.normal(0, 0.02, (n, k))), n, k, Q4K, dev)
+    x = torch.zeros((300, k), dtype=torch.float32, device=dev)
+    y = torch.zeros((300, n), dtype=torch.float32, device=dev)
+    from xn_amd import _lib
+
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    with pytest.raises(XnqError, match="inside a stream capture"):
+        with capture(stream):
+            st = _lib.load().xnq_qtensor_matmul_t(qt.storage.handle, 300, k, n, x.data_ptr(), y.data_ptr(),
+                                                  stream.cuda_stream)
+            _lib.check(st)

@@ -43,6 +43,11 @@ SIGNATURES = {
     "xnq_matmul_t_group_workspace_size": (c_size, [ctypes.POINTER(c_void), c_size, c_size]),
     "xnq_matmul_t_group": (c_int, [ctypes.POINTER(c_void), c_size, c_size, c_size, c_void, ctypes.POINTER(c_void), c_void,
                                    c_size, c_void]),
+    "xnq_capture_begin": (c_int, [c_void]),
+    "xnq_capture_end": (c_int, [c_void, ctypes.POINTER(c_void)]),
+    "xnq_capture_abort": (None, [c_void]),
+    "xnq_graph_launch": (c_int, [c_void, c_void]),
+    "xnq_graph_free": (None, [c_void]),
     "xnq_lhs_workspace_size": (c_size, [c_u32, c_size, c_size]),
     "xnq_qtensor_workspace_size": (c_size, [c_void, c_size]),
     "xnq_quantize_lhs": (c_int, [c_u32, c_size, c_size, c_void, c_void, c_void]),

@@ -196,7 +196,7 @@ extern "C" {
 
 const char* xnq_last_error(void) { return g_err.c_str(); }
 
-int xnq_abi_version(void) { return 3; }
+int xnq_abi_version(void) { return 4; }
 
 size_t xnq_type_size(uint32_t dtype) { return type_size(dtype); }
 size_t xnq_block_size(uint32_t dtype) { return block_size(dtype); }
@@ -467,6 +467,12 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(XNQ_ERR_INVALID,
+                    "matmul_t would allocate its workspace inside a stream capture: use matmul_t_ws with a "
+                    "workspace of xnq_qtensor_matmul_t_workspace_size(qt, %zu) = %zu bytes",
+                    m, ws_bytes);
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, ws_bytes, s);
     if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(workspace)");
@@ -651,6 +657,59 @@ xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* w
     hipError_t e = launch_block_ints(w, a, m, out_dev, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "block_ints");
     return XNQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Stream capture into a replayable graph (xn's Device::capture_begin /
+// capture_end / CaptureGraph::launch, cuda_backend/mod.rs:251-283).
+
+struct xnq_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+xnq_status xnq_capture_begin(void* stream) {
+    if (!stream) return fail(XNQ_ERR_INVALID, "stream capture needs a stream other than the null stream");
+    const hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+    return XNQ_OK;
+}
+
+xnq_status xnq_capture_end(void* stream, xnq_graph** out) {
+    if (!out) return fail(XNQ_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    if (!g) return fail(XNQ_ERR_INVALID, "stream capture ended without a graph");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = new xnq_graph{g, x};
+    return XNQ_OK;
+}
+
+void xnq_capture_abort(void* stream) {
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture((hipStream_t)stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();  // errors of the discarded capture are dropped
+}
+
+xnq_status xnq_graph_launch(const xnq_graph* g, void* stream) {
+    if (!g) return fail(XNQ_ERR_INVALID, "null graph");
+    const hipError_t e = hipGraphLaunch(g->exec, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+    return XNQ_OK;
+}
+
+void xnq_graph_free(xnq_graph* g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
 }
 
 }  // extern "C"

@@ -270,6 +270,21 @@ class QTensor:
         check(L.xnq_qtensor_matmul_t_ws(h, m, k, n, _ptr(lhs), _ptr(ws) if ws is not None else None, nbytes,
                                         _ptr(dst), _stream(self.device)))
 
+    def matmul_t_workspace_size(self, m: int) -> int:
+        """Bytes of caller scratch matmul_t_ws needs for m rows (0 on the decode route)."""
+        return int(_lib.load().xnq_qtensor_matmul_t_workspace_size(self.storage.handle, int(m)))
+
+    def matmul_t_ws(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, ws: Optional[torch.Tensor],
+                    dst: torch.Tensor) -> None:
+        """matmul_t with caller-owned scratch `ws` (uint8, at least
+        matmul_t_workspace_size(m) bytes): allocates nothing, so it can be
+        captured into a graph."""
+        m, k, n = self._check_mm(mkn, lhs, dst)
+        nbytes = ws.numel() if ws is not None else 0
+        check(_lib.load().xnq_qtensor_matmul_t_ws(self.storage.handle, m, k, n, _ptr(lhs),
+                                                  _ptr(ws) if ws is not None else None, nbytes, _ptr(dst),
+                                                  _stream(self.device)))
+
     def matmul_t_split(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
         """quantize_lhs then matmul_preq as two library calls, for every m
         (k_quants.rs:2014-2026: quantize_lhs, then T::matmul)."""
@@ -400,6 +415,56 @@ def matmul_t_group(qts, m: int, k: int, lhs: torch.Tensor, dsts) -> None:
     ws = torch.empty(nbytes, dtype=torch.uint8, device=lhs.device) if nbytes else None
     check(L.xnq_matmul_t_group(hs, len(qts), m, k, _ptr(lhs), ds, _ptr(ws) if ws is not None else None, nbytes,
                                _stream(lhs.device)))
+
+
+# -- stream capture (cuda_backend/mod.rs:251-283: capture_begin / capture_end) --
+
+class CaptureGraph:
+    """A captured sequence of library launches, replayed with launch()."""
+
+    def __init__(self, handle: int, device):
+        self.handle = handle
+        self.device = device
+
+    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        s = stream.cuda_stream if stream is not None else _stream(self.device)
+        check(_lib.load().xnq_graph_launch(self.handle, s))
+
+    def __del__(self):
+        h, self.handle = getattr(self, "handle", None), None
+        if h:
+            _lib.load().xnq_graph_free(h)
+
+
+class capture:
+    """with capture(stream) as c: <library calls on stream>; then c.graph.launch().
+
+    The calls inside are recorded, not run (Device::capture_begin /
+    capture_end); use the entry points that allocate nothing (matmul_t on the
+    decode route, matmul_t_ws, the group / gate entries with workspaces)."""
+
+    def __init__(self, stream: torch.cuda.Stream):
+        self.stream = stream
+        self.graph: Optional[CaptureGraph] = None
+
+    def __enter__(self) -> "capture":
+        self._ctx = torch.cuda.stream(self.stream)
+        self._ctx.__enter__()
+        check(_lib.load().xnq_capture_begin(self.stream.cuda_stream))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> bool:
+        L = _lib.load()
+        try:
+            if exc_type is not None:
+                L.xnq_capture_abort(self.stream.cuda_stream)
+                return False
+            out = ctypes.c_void_p()
+            check(L.xnq_capture_end(self.stream.cuda_stream, ctypes.byref(out)))
+            self.graph = CaptureGraph(out.value, self.stream.device)
+            return False
+        finally:
+            self._ctx.__exit__(exc_type, exc, tb)
 
 
 # -- lower-level entry points used by tests and the benchmark ------------------
