@@ -16,9 +16,11 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "build", "liboracle.so")
 
-Q4_0, Q8_0, Q4K, Q6K, Q8K = 2, 8, 12, 14, 15
-TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292}
-BLOCK_SIZE = {Q4_0: 32, Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1 = 2, 3, 6, 7, 8, 9
+Q2K, Q3K, Q4K, Q5K, Q6K, Q8K = 10, 11, 12, 13, 14, 15
+TYPE_SIZE = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34, Q8_1: 36,
+             Q2K: 84, Q3K: 110, Q4K: 144, Q5K: 176, Q6K: 210, Q8K: 292}
+BLOCK_SIZE = {t: (32 if t <= Q8_1 else 256) for t in TYPE_SIZE}
 
 _lib = None
 
@@ -50,6 +52,12 @@ def lib() -> ctypes.CDLL:
         L.orc_matmul.restype = i
         L.orc_matmul.argtypes = [i, sz, sz, sz, vp, vp, vp]
         L.orc_q4k_block_ints.argtypes = [vp, vp, vp]
+        L.orc_q2k_block_ints.argtypes = [vp, vp, vp]
+        L.orc_q3k_block_ints.argtypes = [vp, vp, vp, vp]
+        L.orc_q5k_block_ints.argtypes = [vp, vp, vp, vp]
+        L.orc_q3k_scales.argtypes = [vp, vp]
+        L.orc_make_q3_quants.restype = ctypes.c_float
+        L.orc_make_q3_quants.argtypes = [vp, i, i, i, vp]
         L.orc_q6k_block_ints.argtypes = [vp, vp, vp]
         L.orc_get_scale_min_k4.argtypes = [i, vp, vp]
         L.orc_q4k_unpack_scales_kmask.argtypes = [vp, vp, vp]
@@ -79,7 +87,12 @@ def nbytes(dt: int, nelem: int) -> int:
 
 
 def vec_dot_type(dt: int) -> int:
-    return Q8_0 if dt in (Q4_0, Q8_0) else Q8K
+    """k_quants.rs: the VecDotType of each weight type."""
+    if dt in (Q4_0, Q5_0, Q8_0):
+        return Q8_0
+    if dt in (Q4_1, Q5_1):
+        return Q8_1
+    return Q8K
 
 
 def from_float(dt: int, x) -> np.ndarray:
@@ -136,9 +149,12 @@ def block_ints(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: i
     vt = vec_dot_type(dt)
     out = np.zeros((m, n, nb, 2), dtype=np.int64)
     wv = w_blocks.reshape(n, nb, TYPE_SIZE[dt])
-    if dt in (Q4K, Q6K):
+    if dt in (Q2K, Q3K, Q4K, Q5K, Q6K):
         av = a_blocks.reshape(m, nb, TYPE_SIZE[vt])
-        fn = lib().orc_q4k_block_ints if dt == Q4K else lib().orc_q6k_block_ints
+        L = lib()
+        fn = {Q2K: L.orc_q2k_block_ints, Q4K: L.orc_q4k_block_ints, Q6K: L.orc_q6k_block_ints,
+              Q3K: lambda w, a, o: L.orc_q3k_block_ints(w, a, o, None),
+              Q5K: lambda w, a, o: L.orc_q5k_block_ints(w, a, o, None)}[dt]
         tmp = np.zeros(2, dtype=np.int64)
         for r in range(m):
             for c in range(n):

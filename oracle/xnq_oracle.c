@@ -37,7 +37,31 @@
 #define QK4_0 32
 
 /* GGML type ids, mod.rs:97-137 */
-enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4K = 12, ORC_Q6K = 14, ORC_Q8K = 15 };
+enum {
+    ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7, ORC_Q8_0 = 8, ORC_Q8_1 = 9,
+    ORC_Q2K = 10, ORC_Q3K = 11, ORC_Q4K = 12, ORC_Q5K = 13, ORC_Q6K = 14, ORC_Q8K = 15
+};
+
+/* xnq_oracle_more.c: Q4_1, Q5_0, Q5_1, Q8_1, Q2_K, Q3_K, Q5_K */
+void orc_q8_1_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q4_1_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q4_1_to_float(const void* in, float* ys, size_t nblocks);
+float orc_q4_1_vec_dot(size_t n, const void* xv, const void* yv);
+void orc_q5_0_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q5_0_to_float(const void* in, float* ys, size_t nblocks);
+float orc_q5_0_vec_dot(size_t n, const void* xv, const void* yv);
+void orc_q5_1_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q5_1_to_float(const void* in, float* ys, size_t nblocks);
+float orc_q5_1_vec_dot(size_t n, const void* xv, const void* yv);
+void orc_q2k_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q2k_to_float(const void* in, float* ys, size_t nblocks);
+float orc_q2k_vec_dot(size_t n, const void* xv, const void* yv);
+void orc_q3k_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q3k_to_float(const void* in, float* ys, size_t nblocks);
+float orc_q3k_vec_dot(size_t n, const void* xv, const void* yv);
+void orc_q5k_from_float(const float* xs, void* out, size_t nblocks);
+void orc_q5k_to_float(const void* in, float* ys, size_t nblocks);
+float orc_q5k_vec_dot(size_t n, const void* xv, const void* yv);
 
 #pragma pack(push, 1)
 typedef struct { uint16_t d; uint8_t qs[16]; } blk_q4_0;
@@ -737,26 +761,47 @@ float orc_q6k_vec_dot(size_t n, const void* xv, const void* yv) {
 static size_t type_size(int dt) {
     switch (dt) {
     case ORC_Q4_0: return 18;
+    case ORC_Q4_1: return 20;
+    case ORC_Q5_0: return 22;
+    case ORC_Q5_1: return 24;
     case ORC_Q8_0: return 34;
+    case ORC_Q8_1: return 36;
+    case ORC_Q2K: return 84;
+    case ORC_Q3K: return 110;
     case ORC_Q4K: return 144;
+    case ORC_Q5K: return 176;
     case ORC_Q6K: return 210;
     case ORC_Q8K: return 292;
     }
     return 0;
 }
-static size_t block_size(int dt) { return (dt == ORC_Q4_0 || dt == ORC_Q8_0) ? 32 : 256; }
+static size_t block_size(int dt) { return dt <= ORC_Q8_1 ? 32 : 256; }
 
 size_t orc_type_size(int dt) { return type_size(dt); }
 size_t orc_block_size(int dt) { return block_size(dt); }
 
-/* The activation ("vec dot") type of each weight type, k_quants.rs:210,615,1321,1727. */
-int orc_vec_dot_type(int dt) { return (dt == ORC_Q4_0 || dt == ORC_Q8_0) ? ORC_Q8_0 : ORC_Q8K; }
+/* The activation ("vec dot") type of each weight type, k_quants.rs:210, 310,
+ * 405, 507, 615, 883, 1059, 1321, 1510, 1727. */
+int orc_vec_dot_type(int dt) {
+    switch (dt) {
+    case ORC_Q4_0: case ORC_Q5_0: case ORC_Q8_0: return ORC_Q8_0;
+    case ORC_Q4_1: case ORC_Q5_1: return ORC_Q8_1;
+    }
+    return ORC_Q8K;
+}
 
 int orc_from_float(int dt, const float* xs, void* out, size_t nblocks) {
     switch (dt) {
     case ORC_Q4_0: orc_q4_0_from_float(xs, out, nblocks); return 0;
+    case ORC_Q4_1: orc_q4_1_from_float(xs, out, nblocks); return 0;
+    case ORC_Q5_0: orc_q5_0_from_float(xs, out, nblocks); return 0;
+    case ORC_Q5_1: orc_q5_1_from_float(xs, out, nblocks); return 0;
     case ORC_Q8_0: orc_q8_0_from_float(xs, out, nblocks); return 0;
+    case ORC_Q8_1: orc_q8_1_from_float(xs, out, nblocks); return 0;
+    case ORC_Q2K: orc_q2k_from_float(xs, out, nblocks); return 0;
+    case ORC_Q3K: orc_q3k_from_float(xs, out, nblocks); return 0;
     case ORC_Q4K: orc_q4k_from_float(xs, out, nblocks); return 0;
+    case ORC_Q5K: orc_q5k_from_float(xs, out, nblocks); return 0;
     case ORC_Q6K: orc_q6k_from_float(xs, out, nblocks); return 0;
     case ORC_Q8K: orc_q8k_from_float(xs, out, nblocks); return 0;
     }
@@ -766,8 +811,14 @@ int orc_from_float(int dt, const float* xs, void* out, size_t nblocks) {
 int orc_to_float(int dt, const void* in, float* ys, size_t nblocks) {
     switch (dt) {
     case ORC_Q4_0: orc_q4_0_to_float(in, ys, nblocks); return 0;
+    case ORC_Q4_1: orc_q4_1_to_float(in, ys, nblocks); return 0;
+    case ORC_Q5_0: orc_q5_0_to_float(in, ys, nblocks); return 0;
+    case ORC_Q5_1: orc_q5_1_to_float(in, ys, nblocks); return 0;
     case ORC_Q8_0: orc_q8_0_to_float(in, ys, nblocks); return 0;
+    case ORC_Q2K: orc_q2k_to_float(in, ys, nblocks); return 0;
+    case ORC_Q3K: orc_q3k_to_float(in, ys, nblocks); return 0;
     case ORC_Q4K: orc_q4k_to_float(in, ys, nblocks); return 0;
+    case ORC_Q5K: orc_q5k_to_float(in, ys, nblocks); return 0;
     case ORC_Q6K: orc_q6k_to_float(in, ys, nblocks); return 0;
     case ORC_Q8K: orc_q8k_to_float(in, ys, nblocks); return 0;
     }
@@ -777,8 +828,14 @@ int orc_to_float(int dt, const void* in, float* ys, size_t nblocks) {
 float orc_vec_dot(int dt, size_t k, const void* w_row, const void* a_row) {
     switch (dt) {
     case ORC_Q4_0: return orc_q4_0_vec_dot(k, w_row, a_row);
+    case ORC_Q4_1: return orc_q4_1_vec_dot(k, w_row, a_row);
+    case ORC_Q5_0: return orc_q5_0_vec_dot(k, w_row, a_row);
+    case ORC_Q5_1: return orc_q5_1_vec_dot(k, w_row, a_row);
     case ORC_Q8_0: return orc_q8_0_vec_dot(k, w_row, a_row);
+    case ORC_Q2K: return orc_q2k_vec_dot(k, w_row, a_row);
+    case ORC_Q3K: return orc_q3k_vec_dot(k, w_row, a_row);
     case ORC_Q4K: return orc_q4k_vec_dot(k, w_row, a_row);
+    case ORC_Q5K: return orc_q5k_vec_dot(k, w_row, a_row);
     case ORC_Q6K: return orc_q6k_vec_dot(k, w_row, a_row);
     }
     return NAN;
@@ -801,6 +858,9 @@ int orc_matmul_preq(int dt, size_t m, size_t k, size_t n, const void* lhs_b, con
     int vt = orc_vec_dot_type(dt);
     size_t bs = block_size(dt);
     if (k % bs) return -1;
+    /* vec_dot_q4_1_q8_1 / q5_0_q8_0 / q5_1_q8_1: "nb is not divisible by 2"
+     * (k_quants.rs:323-325, 413-415, 519-521) */
+    if ((dt == ORC_Q4_1 || dt == ORC_Q5_0 || dt == ORC_Q5_1) && (k / bs) % 2) return -3;
     size_t kb_w = k / bs, kb_a = k / block_size(vt);
     size_t ws = type_size(dt), as = type_size(vt);
     for (size_t r = 0; r < m; r++) {

@@ -174,3 +174,157 @@ def block_ints_bruteforce(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m
         sub = np.einsum("mbje,nbje->mnbj", qa16, q)
         out[..., 0] = np.einsum("mnbj,nbj->mnb", sub, sc)
     return out
+
+
+# --------------------------------------------- Q4_1, Q5_0, Q5_1, Q8_1
+def _f16_field(b: np.ndarray, off: int) -> np.ndarray:
+    return _f16_from_bits(b[:, off:off + 2].copy().view(np.uint16)[:, 0])
+
+
+def decode_q4_1(blocks: np.ndarray):
+    """-> d, m f32 [nb], q int64 [nb, 32] in 0..15; y = q*d + m"""
+    b = blocks.reshape(-1, 20)
+    qs = b[:, 4:].astype(np.int64)
+    return _f16_field(b, 0), _f16_field(b, 2), np.concatenate([qs & 0xF, qs >> 4], axis=1)
+
+
+def _fifth_bits(qh_bytes: np.ndarray) -> np.ndarray:
+    """u32 little endian qh -> bit e of it for e = 0..31, as int64 [nb, 32]."""
+    qh = qh_bytes.copy().view(np.uint32)[:, 0].astype(np.int64)
+    return (qh[:, None] >> np.arange(32)[None, :]) & 1
+
+
+def decode_q5_0(blocks: np.ndarray):
+    """-> d f32 [nb], q int64 [nb, 32] in -16..15"""
+    b = blocks.reshape(-1, 22)
+    qs = b[:, 6:].astype(np.int64)
+    lo = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+    return _f16_field(b, 0), (lo | (_fifth_bits(b[:, 2:6]) << 4)) - 16
+
+
+def decode_q5_1(blocks: np.ndarray):
+    """-> d, m f32 [nb], q int64 [nb, 32] in 0..31"""
+    b = blocks.reshape(-1, 24)
+    qs = b[:, 8:].astype(np.int64)
+    lo = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+    return _f16_field(b, 0), _f16_field(b, 2), lo | (_fifth_bits(b[:, 4:8]) << 4)
+
+
+def decode_q8_1(blocks: np.ndarray):
+    """-> d, s f32 [nb], q int64 [nb, 32]"""
+    b = blocks.reshape(-1, 36)
+    return _f16_field(b, 0), _f16_field(b, 2), b[:, 4:].view(np.int8).astype(np.int64)
+
+
+# --------------------------------------------------------- Q2_K, Q3_K, Q5_K
+# Element e of a super-block, e = 128*h + 32*t + l (h half, t 2-bit plane):
+#   Q2K / Q3K low bits: qs[32*h + l] >> 2t & 3; Q3K high bit: hmask[l] bit 4h + t.
+#   Q5K: e = 64*i + 32*s + l: low nibble of qs[32*i + l] (s = 0) or high (s = 1),
+#   fifth bit qh[l] bit 2i + s.
+def encode_q2k(d_bits: int, dmin_bits: int, sc, mn, q) -> np.ndarray:
+    """sc, mn [16] in 0..15; q [256] in 0..3."""
+    q = np.asarray(q, np.int64)
+    out = np.zeros(84, np.uint8)
+    out[0:16] = (np.asarray(sc, np.int64) & 15) | ((np.asarray(mn, np.int64) & 15) << 4)
+    for e in range(256):
+        h, t, l = e // 128, (e % 128) // 32, e % 32
+        out[16 + 32 * h + l] |= (q[e] & 3) << (2 * t)
+    out[80:82] = np.array([d_bits], np.uint16).view(np.uint8)
+    out[82:84] = np.array([dmin_bits], np.uint16).view(np.uint8)
+    return out
+
+
+def decode_q2k(blocks: np.ndarray):
+    """-> d, dmin f32 [nb]; sc, mn int64 [nb, 16]; q int64 [nb, 256] in 0..3"""
+    b = blocks.reshape(-1, 84)
+    nb = b.shape[0]
+    sc = b[:, 0:16].astype(np.int64)
+    q = np.zeros((nb, 256), np.int64)
+    qs = b[:, 16:80].astype(np.int64)
+    for e in range(256):
+        h, t, l = e // 128, (e % 128) // 32, e % 32
+        q[:, e] = (qs[:, 32 * h + l] >> (2 * t)) & 3
+    return _f16_field(b, 80), _f16_field(b, 82), sc & 15, sc >> 4, q
+
+
+def pack_scales_q3k(sc) -> np.ndarray:
+    """16 six-bit scales (0..63) -> 12 bytes: low nibbles of scales j and j + 8
+    in byte j (j < 8), the top 2 bits of scale j in byte 8 + j % 4 at bit 2*(j // 4)."""
+    sc = np.asarray(sc, np.int64)
+    out = np.zeros(12, np.int64)
+    for j in range(16):
+        if j < 8:
+            out[j] |= sc[j] & 15
+        else:
+            out[j - 8] |= (sc[j] & 15) << 4
+        out[8 + j % 4] |= (sc[j] >> 4) << (2 * (j // 4))
+    return out.astype(np.uint8)
+
+
+def unpack_scales_q3k(b12: np.ndarray) -> np.ndarray:
+    b = b12.astype(np.int64)
+    sc = np.zeros(16, np.int64)
+    for j in range(16):
+        lo = (b[j] & 15) if j < 8 else (b[j - 8] >> 4)
+        sc[j] = lo | (((b[8 + j % 4] >> (2 * (j // 4))) & 3) << 4)
+    return sc
+
+
+def encode_q3k(d_bits: int, sc, q) -> np.ndarray:
+    """sc [16] in 0..63 (scale + 32); q [256] in -4..3."""
+    q = np.asarray(q, np.int64) + 4  # 0..7
+    out = np.zeros(110, np.uint8)
+    for e in range(256):
+        h, t, l = e // 128, (e % 128) // 32, e % 32
+        out[32 + 32 * h + l] |= (q[e] & 3) << (2 * t)
+        if q[e] & 4:
+            out[l] |= 1 << (4 * h + t)
+    out[96:108] = pack_scales_q3k(sc)
+    out[108:110] = np.array([d_bits], np.uint16).view(np.uint8)
+    return out
+
+
+def decode_q3k(blocks: np.ndarray):
+    """-> d f32 [nb]; sc int64 [nb, 16] in -32..31; q int64 [nb, 256] in -4..3"""
+    b = blocks.reshape(-1, 110)
+    nb = b.shape[0]
+    sc = np.stack([unpack_scales_q3k(b[i, 96:108]) for i in range(nb)]) - 32
+    q = np.zeros((nb, 256), np.int64)
+    hm = b[:, 0:32].astype(np.int64)
+    qs = b[:, 32:96].astype(np.int64)
+    for e in range(256):
+        h, t, l = e // 128, (e % 128) // 32, e % 32
+        q[:, e] = ((qs[:, 32 * h + l] >> (2 * t)) & 3) | (((hm[:, l] >> (4 * h + t)) & 1) << 2)
+    return _f16_field(b, 108), sc, q - 4
+
+
+def encode_q5k(d_bits: int, dmin_bits: int, sc, mn, q) -> np.ndarray:
+    """sc, mn [8] in 0..63; q [256] in 0..31."""
+    q = np.asarray(q, np.int64)
+    out = np.zeros(176, np.uint8)
+    out[0:2] = np.array([d_bits], np.uint16).view(np.uint8)
+    out[2:4] = np.array([dmin_bits], np.uint16).view(np.uint8)
+    out[4:16] = pack_scales_k4(np.asarray(sc, np.int64), np.asarray(mn, np.int64))
+    for e in range(256):
+        i, s, l = e // 64, (e % 64) // 32, e % 32
+        out[48 + 32 * i + l] |= (q[e] & 15) << (4 * s)
+        if q[e] & 16:
+            out[16 + l] |= 1 << (2 * i + s)
+    return out
+
+
+def decode_q5k(blocks: np.ndarray):
+    """-> d, dmin f32 [nb]; sc, mn int64 [nb, 8]; q int64 [nb, 256] in 0..31"""
+    b = blocks.reshape(-1, 176)
+    nb = b.shape[0]
+    sc = np.zeros((nb, 8), np.int64)
+    mn = np.zeros((nb, 8), np.int64)
+    for i in range(nb):
+        sc[i], mn[i] = unpack_scales_k4(b[i, 4:16])
+    qh = b[:, 16:48].astype(np.int64)
+    qs = b[:, 48:176].astype(np.int64)
+    q = np.zeros((nb, 256), np.int64)
+    for e in range(256):
+        i, s, l = e // 64, (e % 64) // 32, e % 32
+        q[:, e] = ((qs[:, 32 * i + l] >> (4 * s)) & 15) | (((qh[:, l] >> (2 * i + s)) & 1) << 4)
+    return _f16_field(b, 0), _f16_field(b, 2), sc, mn, q
