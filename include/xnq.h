@@ -38,8 +38,15 @@ enum {
     XNQ_F32 = 0,
     XNQ_F16 = 1,
     XNQ_Q4_0 = 2,
+    XNQ_Q4_1 = 3,
+    XNQ_Q5_0 = 6,
+    XNQ_Q5_1 = 7,
     XNQ_Q8_0 = 8,
+    XNQ_Q8_1 = 9,
+    XNQ_Q2K = 10,
+    XNQ_Q3K = 11,
     XNQ_Q4K = 12,
+    XNQ_Q5K = 13,
     XNQ_Q6K = 14,
     XNQ_Q8K = 15
 };

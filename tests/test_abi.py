@@ -55,7 +55,7 @@ def test_host_validation(lib):
     st = lib.xnq_qtensor_upload(0, 99, None, 1, 256, None, ctypes.byref(out))
     assert st == 1 and b"unknown dtype" in lib.xnq_last_error()
     # dtype without a device implementation (lib.rs:284-287)
-    st = lib.xnq_qtensor_upload(0, 10, None, 1, 256, None, ctypes.byref(out))
+    st = lib.xnq_qtensor_upload(0, 30, None, 1, 256, None, ctypes.byref(out))
     assert st == 2 and b"not supported" in lib.xnq_last_error()
     # last dim not divisible by the block size (mod.rs:262-274)
     st = lib.xnq_qtensor_upload(0, 12, None, 1, 100, None, ctypes.byref(out))

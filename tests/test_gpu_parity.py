@@ -243,7 +243,7 @@ def test_errors(orc, dev):
     with pytest.raises(XnqError, match="divisible"):
         QTensor.from_gguf_bytes(blocks, (8, 128), GgmlDType.Q4K, dev)
     with pytest.raises(XnqError, match="not supported"):
-        QTensor.from_gguf_bytes(np.zeros(84, np.uint8), (1, 256), GgmlDType.Q2K, dev)
+        QTensor.from_gguf_bytes(np.zeros(512, np.uint8), (1, 256), GgmlDType.F16, dev)
     qt = QTensor.from_gguf_bytes(blocks, (4, 256), GgmlDType.Q4K, dev)
     lhs = torch.zeros(512, device=dev)
     dst = torch.zeros(8, device=dev)

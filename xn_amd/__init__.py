@@ -9,9 +9,15 @@ from . import gguf  # noqa: F401
 from .quantized import (  # noqa: F401
     DEVICE_DTYPES,
     GgmlDType,
+    Q2kHip,
+    Q3kHip,
     Q4kHip,
+    Q5kHip,
     Q6kHip,
     Q40Hip,
+    Q41Hip,
+    Q50Hip,
+    Q51Hip,
     Q80Hip,
     QLinear,
     QStorage,
@@ -21,5 +27,5 @@ from .quantized import (  # noqa: F401
 
 __all__ = [
     "XnqError", "load", "GgmlDType", "QTensor", "QStorage", "QLinear", "Q40Hip", "Q80Hip",
-    "Q4kHip", "Q6kHip", "DEVICE_DTYPES", "vec_dot_type", "gguf",
+    "Q4kHip", "Q6kHip", "Q41Hip", "Q50Hip", "Q51Hip", "Q2kHip", "Q3kHip", "Q5kHip", "DEVICE_DTYPES", "vec_dot_type", "gguf",
 ]

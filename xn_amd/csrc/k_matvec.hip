@@ -80,6 +80,12 @@ hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hip
     case XNQ_Q4_0: return launch_matvec_q4_0(w, a, nullptr, m, y, s, false);
     case XNQ_Q4K: return launch_matvec_q4k(w, a, nullptr, m, y, s, false);
     case XNQ_Q6K: return launch_matvec_q6k(w, a, nullptr, m, y, s, false);
+    case XNQ_Q4_1: return launch_matvec_q4_1(w, a, nullptr, m, y, s, false);
+    case XNQ_Q5_0: return launch_matvec_q5_0(w, a, nullptr, m, y, s, false);
+    case XNQ_Q5_1: return launch_matvec_q5_1(w, a, nullptr, m, y, s, false);
+    case XNQ_Q2K: return launch_matvec_q2k(w, a, nullptr, m, y, s, false);
+    case XNQ_Q3K: return launch_matvec_q3k(w, a, nullptr, m, y, s, false);
+    case XNQ_Q5K: return launch_matvec_q5k(w, a, nullptr, m, y, s, false);
     }
     return hipErrorInvalidValue;
 }
@@ -88,12 +94,18 @@ hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* 
     AView a{};
     a.k = w.k;
     a.m = (uint32_t)m;
-    a.A = act_img(w.k, w.dtype == XNQ_Q4K || w.dtype == XNQ_Q6K);
+    a.A = act_img(w.k, is_kquant(w.dtype));
     switch (w.dtype) {
     case XNQ_Q8_0: return launch_matvec_q8_0(w, a, x, m, y, s, true);
     case XNQ_Q4_0: return launch_matvec_q4_0(w, a, x, m, y, s, true);
     case XNQ_Q4K: return launch_matvec_q4k(w, a, x, m, y, s, true);
     case XNQ_Q6K: return launch_matvec_q6k(w, a, x, m, y, s, true);
+    case XNQ_Q4_1: return launch_matvec_q4_1(w, a, x, m, y, s, true);
+    case XNQ_Q5_0: return launch_matvec_q5_0(w, a, x, m, y, s, true);
+    case XNQ_Q5_1: return launch_matvec_q5_1(w, a, x, m, y, s, true);
+    case XNQ_Q2K: return launch_matvec_q2k(w, a, x, m, y, s, true);
+    case XNQ_Q3K: return launch_matvec_q3k(w, a, x, m, y, s, true);
+    case XNQ_Q5K: return launch_matvec_q5k(w, a, x, m, y, s, true);
     }
     return hipErrorInvalidValue;
 }
@@ -104,11 +116,18 @@ hipError_t launch_matvec_group(const WGroup& g, const float* x, bool gate, hipSt
     case XNQ_Q4_0: return launch_group_q4_0(g, x, gate, s);
     case XNQ_Q4K: return launch_group_q4k(g, x, gate, s);
     case XNQ_Q6K: return launch_group_q6k(g, x, gate, s);
+    case XNQ_Q4_1: return launch_group_q4_1(g, x, gate, s);
+    case XNQ_Q5_0: return launch_group_q5_0(g, x, gate, s);
+    case XNQ_Q5_1: return launch_group_q5_1(g, x, gate, s);
+    case XNQ_Q2K: return launch_group_q2k(g, x, gate, s);
+    case XNQ_Q3K: return launch_group_q3k(g, x, gate, s);
+    case XNQ_Q5K: return launch_group_q5k(g, x, gate, s);
     }
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_block_ints(const WView& w, const AView& a, size_t m, int32_t* out, hipStream_t s) {
+    if (is_raw_layout(w.dtype)) return hipErrorNotSupported;
     const size_t total = m * w.n * w.nb;
     if (total == 0) return hipSuccess;
     block_ints_kernel<<<(unsigned)((total + 127) / 128), 128, 0, s>>>(w, a, (uint32_t)m, out);

@@ -88,7 +88,7 @@ __device__ void stage_activations(const AView& a, uint32_t m0, uint32_t mcount, 
 // weight stream.
 template <int DT, int MB, int kNW, int kBatch>
 struct XQuant {
-    static constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    static constexpr bool kq = is_kquant(DT);
     float4 v[kBatch];
     // first block of round 0 for this wavefront, and the block step between rounds
     __device__ __forceinline__ static uint32_t first(uint32_t wave) { return kq ? wave : wave * 8; }
@@ -146,6 +146,9 @@ struct Chunk {
     uint4 q;
     uint4 x;  // Q8_0: second 16 bytes; Q4K: {d|dmin, scales}; Q6K: qh in .x/.y, scale pair in .z
     float dw;
+    // the padded-block types: the chunk's low bits (Q2K/Q3K/Q5K: 32 bytes in
+    // q, e0), its high bits (Q3K hmask / Q5K qh: 32 bytes in e1, e2)
+    uint4 e0, e1, e2;
 };
 
 // Byte offsets are 32-bit (every plane is < 4 GiB, checked at upload), so the
@@ -178,7 +181,7 @@ __device__ __forceinline__ void load_chunk(const WView& w, uint32_t row, uint32_
     } else if (DT == XNQ_Q4K) {
         ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
         ch.x = ldw(reinterpret_cast<const uint4*>(w.s + (row * w.s_row + (c >> 3) * 16)));
-    } else {  // Q6K
+    } else if (DT == XNQ_Q6K) {
         const uint32_t sb = c >> 3, j = c & 7;
         ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
         const uint2 h = ldw(reinterpret_cast<const uint2*>(w.h + (row * w.h_row + c * 8)));
@@ -186,19 +189,159 @@ __device__ __forceinline__ void load_chunk(const WView& w, uint32_t row, uint32_
         ch.x.y = h.y;
         ch.x.z = ldw(reinterpret_cast<const uint16_t*>(w.s + (row * w.s_row + sb * 16 + 2 * j)));
         ch.dw = f16_bits_to_f32(ldw(reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + sb * 2))));
+    } else {
+        // padded GGUF blocks: every field is dword aligned (raw_stride), the
+        // loads are dword loads
+        const uint32_t* b;
+        if (!is_kquant(DT)) {
+            b = reinterpret_cast<const uint32_t*>(w.q + row * w.q_row + c * raw_stride(DT));
+            ch.x.x = b[0];  // d | m (Q4_1, Q5_1) or d (Q5_0)
+            const uint32_t o = DT == XNQ_Q4_1 ? 1 : 2;
+            if (DT != XNQ_Q4_1) ch.x.y = b[1];  // qh
+            ch.q = make_uint4(b[o], b[o + 1], b[o + 2], b[o + 3]);
+            return;
+        }
+        const uint32_t j = c & 7;
+        b = reinterpret_cast<const uint32_t*>(w.q + row * w.q_row + (c >> 3) * raw_stride(DT));
+        auto ld8 = [&](uint32_t dw0, uint4& lo, uint4& hi) {
+            lo = make_uint4(b[dw0], b[dw0 + 1], b[dw0 + 2], b[dw0 + 3]);
+            hi = make_uint4(b[dw0 + 4], b[dw0 + 5], b[dw0 + 6], b[dw0 + 7]);
+        };
+        if (DT == XNQ_Q2K) {
+            ld8(4 + 8 * (j >> 2), ch.q, ch.e0);  // qs[32h .. 32h+32)
+            ch.x.x = b[20];                        // d | dmin
+            ch.x.y = b[j >> 1];                    // scales 2j, 2j+1 in half (j & 1)
+        } else if (DT == XNQ_Q3K) {
+            ld8(8 + 8 * (j >> 2), ch.q, ch.e0);  // qs[32h .. 32h+32)
+            ld8(0, ch.e1, ch.e2);                 // hmask
+            ch.x = make_uint4(b[24], b[25], b[26], b[27]);  // scales[12], d
+        } else {  // Q5K
+            ld8(12 + 8 * (j >> 1), ch.q, ch.e0);  // qs[32i .. 32i+32)
+            ld8(4, ch.e1, ch.e2);                  // qh
+            ch.x = make_uint4(b[0], b[1], b[2], b[3]);  // d | dmin, scales[12]
+        }
+    }
+}
+
+// Bytes 4w .. 4w+3 of a 32-byte run held as two uint4.
+__device__ __forceinline__ uint32_t dw_of(const uint4& lo, const uint4& hi, int w) {
+    const uint4& v = w < 4 ? lo : hi;
+    const int i = w & 3;
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+// The 4 bits at 4w .. 4w+3 of x spread to bit 0 of bytes 0..3.
+__device__ __forceinline__ uint32_t spread4(uint32_t x, int w) {
+    const uint32_t v = (x >> (4 * w)) & 0xFu;
+    return (v & 1u) | ((v & 2u) << 7) | ((v & 4u) << 14) | ((v & 8u) << 21);
+}
+
+// f32 combine of one weight chunk c against one activation chunk: a[8] the
+// 32 int8 (elements 0-15 in a[0..3], 16-31 in a[4..7]), sv the chunk's side
+// word (Q8K: bsum of elements 0-15 | bsum of 16-31 << 16; Q8_0: the block
+// sum), da the activation block scale.  Integer parts are exact; the f32
+// combine follows each type's vec_dot per block.
+template <int DT>
+__device__ __forceinline__ void chunk_fma(const Chunk& ch, uint32_t c, const int* a, int32_t sv, float da,
+                                          float& acc) {
+    const int bs0 = (int)(int16_t)(sv & 0xffff), bs1 = (int)(int16_t)(sv >> 16);
+    if (DT == XNQ_Q4K) {
+        int sc, mn, lo, hi;
+        const float dw = f16_bits_to_f32(ch.x.x), dmin = f16_bits_to_f32(ch.x.x >> 16);
+        q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)(c & 7), sc, mn);
+        nib_dot2(ch.q, a, lo, hi);
+        const int isum = sc * (lo + hi);
+        const int msum = mn * (bs0 + bs1);
+        acc += (dw * da) * (float)isum - (dmin * da) * (float)msum;
+    } else if (DT == XNQ_Q6K) {
+        const int sc0 = (int)(int8_t)(ch.x.z & 0xff), sc1 = (int)(int8_t)((ch.x.z >> 8) & 0xff);
+        const int v = q6k_chunk_int(ch.q, make_uint2(ch.x.x, ch.x.y), a, sc0, sc1, bs0, bs1);
+        acc += (ch.dw * da) * (float)v;
+    } else if (DT == XNQ_Q4_0) {
+        int lo, hi;
+        nib_dot2(ch.q, a, lo, hi);
+        acc += (ch.dw * da) * (float)(lo + hi - 8 * sv);
+    } else if (DT == XNQ_Q8_0) {
+        acc += (ch.dw * da) * (float)i8_dot32(ch.q, ch.x, a);
+    } else if (DT == XNQ_Q4_1 || DT == XNQ_Q5_0 || DT == XNQ_Q5_1) {
+        // k_quants.rs:316-343, 419-440, 513-544
+        int sumi;
+        if (DT == XNQ_Q4_1) {
+            int lo, hi;
+            nib_dot2(ch.q, a, lo, hi);
+            sumi = lo + hi;
+        } else {
+            const uint32_t q4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
+            sumi = 0;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint32_t lo = (q4[w] & 0x0F0F0F0Fu) | (spread4(ch.x.y, w) << 4);
+                const uint32_t hi = ((q4[w] >> 4) & 0x0F0F0F0Fu) | (spread4(ch.x.y >> 16, w) << 4);
+                sumi = dot4((int)lo, a[w], sumi);
+                sumi = dot4((int)hi, a[4 + w], sumi);
+            }
+            if (DT == XNQ_Q5_0) sumi -= 16 * sv;
+        }
+        const float dw = f16_bits_to_f32(ch.x.x);
+        float r = (float)sumi * dw * da;
+        if (DT != XNQ_Q5_0) {
+            // Q8_1's s = f16(f16(sum) * d) (k_quants.rs:871), times the weight's m
+            const float s = f16_bits_to_f32(
+                f32_to_f16_bits(f16_bits_to_f32(f32_to_f16_bits((float)sv)) * da));
+            r = r + f16_bits_to_f32(ch.x.x >> 16) * s;
+        }
+        acc += r;
+    } else if (DT == XNQ_Q2K) {
+        // k_quants.rs:899-948: dall * sum_g (sc_g & 15) isum_g - dmin * sum_g (sc_g >> 4) bsum_g
+        const uint32_t sh = 2 * (c & 3);
+        int i0 = 0, i1 = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            i0 = dot4((int)((dw_of(ch.q, ch.e0, w) >> sh) & 0x03030303u), a[w], i0);
+            i1 = dot4((int)((dw_of(ch.q, ch.e0, w + 4) >> sh) & 0x03030303u), a[4 + w], i1);
+        }
+        const uint32_t scw = (ch.x.y >> (16 * (c & 1))) & 0xffffu;
+        const int s0 = (int)(scw & 0xff), s1 = (int)(scw >> 8);
+        const int isum = (s0 & 15) * i0 + (s1 & 15) * i1;
+        const int summs = bs0 * (s0 >> 4) + bs1 * (s1 >> 4);
+        const float dall = da * f16_bits_to_f32(ch.x.x), dmin = da * f16_bits_to_f32(ch.x.x >> 16);
+        acc += dall * (float)isum - dmin * (float)summs;
+    } else if (DT == XNQ_Q3K) {
+        // k_quants.rs:1071-1152: (q3 & 3) - (hmask bit ? 0 : 4), 16-element groups of scale sc - 32
+        const uint32_t sh = 2 * (c & 3), hb = 4 * ((c & 7) >> 2) + (c & 3);
+        int u0 = 0, u1 = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t l0 = ((dw_of(ch.q, ch.e0, w) >> sh) & 0x03030303u) |
+                                (((dw_of(ch.e1, ch.e2, w) >> hb) & 0x01010101u) << 2);
+            const uint32_t l1 = ((dw_of(ch.q, ch.e0, w + 4) >> sh) & 0x03030303u) |
+                                (((dw_of(ch.e1, ch.e2, w + 4) >> hb) & 0x01010101u) << 2);
+            u0 = dot4((int)l0, a[w], u0);
+            u1 = dot4((int)l1, a[4 + w], u1);
+        }
+        const int g = 2 * (int)(c & 7);
+        const int sc0 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g) - 32;
+        const int sc1 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g + 1) - 32;
+        const int isum = sc0 * (u0 - 4 * bs0) + sc1 * (u1 - 4 * bs1);
+        acc += (f16_bits_to_f32(ch.x.w) * da) * (float)isum;
+    } else {  // Q5K, k_quants.rs:1524-1605
+        const uint32_t j = c & 7, s = j & 1, hb = 2 * (j >> 1) + s;
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t nib = (dw_of(ch.q, ch.e0, w) >> (4 * s)) & 0x0F0F0F0Fu;
+            const uint32_t h5 = ((dw_of(ch.e1, ch.e2, w) >> hb) & 0x01010101u) << 4;
+            v = dot4((int)(nib | h5), a[w], v);
+        }
+        int sc, mn;
+        q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)j, sc, mn);
+        const float d = f16_bits_to_f32(ch.x.x) * da, dmin = f16_bits_to_f32(ch.x.x >> 16) * da;
+        acc += d * (float)(sc * v) - dmin * (float)(mn * (bs0 + bs1));
     }
 }
 
 template <int DT, int MB>
 __device__ __forceinline__ void compute_chunk(const Chunk& ch, uint32_t c, uint32_t k,
                                               const uint8_t* lds, const ActImg& A, float* acc) {
-    int sc = 0, mn = 0;
-    float dw = ch.dw, dmin = 0.0f;
-    if (DT == XNQ_Q4K) {
-        dw = f16_bits_to_f32(ch.x.x);
-        dmin = f16_bits_to_f32(ch.x.x >> 16);
-        q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)(c & 7), sc, mn);
-    }
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const uint8_t* row = lds + mb * A.row_bytes;
@@ -208,28 +351,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk& ch, uint32_t c, uint3
                           (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
         const int32_t sv = reinterpret_cast<const int32_t*>(row + A.s_off)[c];
         const float* ld = reinterpret_cast<const float*>(row + A.d_off);
-        if (DT == XNQ_Q4K) {
-            int lo, hi;
-            nib_dot2(ch.q, a, lo, hi);
-            const int isum = sc * (lo + hi);
-            const int msum = mn * ((int)(int16_t)(sv & 0xffff) + (int)(int16_t)(sv >> 16));
-            const float da = ld[c >> 3];
-            acc[mb] += (dw * da) * (float)isum - (dmin * da) * (float)msum;
-        } else if (DT == XNQ_Q6K) {
-            const int sc0 = (int)(int8_t)(ch.x.z & 0xff), sc1 = (int)(int8_t)((ch.x.z >> 8) & 0xff);
-            const int v = q6k_chunk_int(ch.q, make_uint2(ch.x.x, ch.x.y), a, sc0, sc1,
-                                        (int)(int16_t)(sv & 0xffff), (int)(int16_t)(sv >> 16));
-            const float da = ld[c >> 3];
-            acc[mb] += (dw * da) * (float)v;
-        } else if (DT == XNQ_Q4_0) {
-            int lo, hi;
-            nib_dot2(ch.q, a, lo, hi);
-            const int v = lo + hi - 8 * sv;
-            acc[mb] += (dw * ld[c]) * (float)v;
-        } else {
-            const int v = i8_dot32(ch.q, ch.x, a);
-            acc[mb] += (dw * ld[c]) * (float)v;
-        }
+        chunk_fma<DT>(ch, c, a, sv, ld[is_kquant(DT) ? c >> 3 : c], acc[mb]);
     }
 }
 
@@ -278,7 +400,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
                                                          uint32_t m0, uint32_t mcount,
                                                          float* __restrict__ y) {
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    constexpr bool kq = is_kquant(DT);
     const ActImg A = act_img(w.k, kq);
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = threadIdx.x / kWave;
@@ -371,7 +493,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
 template <int DT, int R, int CPL, int NW, bool GATE>
 __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* __restrict__ x) {
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    constexpr bool kq = is_kquant(DT);
     constexpr int RR = GATE ? 2 * R : R;  // rows loaded per wavefront
     const uint32_t k = G.w[0].k;
     const ActImg A = act_img(k, kq);
@@ -497,7 +619,7 @@ template <int DT, int MB, int R, int CPL, int NW, bool FUSED>
 hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m0, uint32_t mc,
                       float* y, hipStream_t s) {
     static_assert(R * MB <= 64, "one output per lane");
-    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    constexpr bool kq = is_kquant(DT);
     const uint32_t lds = lds_bytes(MB, w.k, kq);
     auto fn = matvec_kernel<DT, MB, R, CPL, NW, FUSED>;
     int ncu = 1;
@@ -512,7 +634,7 @@ hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m
 
 template <int DT, int R, int CPL, bool GATE>
 hipError_t launch_group_one(const WGroup& g, const float* x, hipStream_t s) {
-    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    constexpr bool kq = is_kquant(DT);
     constexpr int NW = 16;
     const uint32_t lds = lds_bytes(1, g.w[0].k, kq);
     auto fn = group_kernel<DT, R, CPL, NW, GATE>;
@@ -626,7 +748,7 @@ inline int pick_rows(uint32_t n, int cpl) {
 template <int DT>
 hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m, float* y,
                         hipStream_t s, bool fused) {
-    constexpr bool kq = (DT == XNQ_Q4K || DT == XNQ_Q6K);
+    constexpr bool kq = is_kquant(DT);
     int gmax = 8;
     while (gmax > 1 && lds_bytes(gmax, w.k, kq) > kMaxLds) gmax >>= 1;
     if (lds_bytes(gmax, w.k, kq) > kMaxLds) return hipErrorInvalidConfiguration;
@@ -670,6 +792,18 @@ hipError_t launch_matvec_q4_0(const WView&, const AView&, const float*, size_t, 
 hipError_t launch_matvec_q8_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
 hipError_t launch_matvec_q4k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
 hipError_t launch_matvec_q6k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q4_1(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q5_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q5_1(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q2k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q3k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q5k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_group_q4_1(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q5_0(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q5_1(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q2k(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q3k(const WGroup&, const float*, bool, hipStream_t);
+hipError_t launch_group_q5k(const WGroup&, const float*, bool, hipStream_t);
 hipError_t launch_group_q4_0(const WGroup&, const float*, bool, hipStream_t);
 hipError_t launch_group_q8_0(const WGroup&, const float*, bool, hipStream_t);
 hipError_t launch_group_q4k(const WGroup&, const float*, bool, hipStream_t);

@@ -1,0 +1,15 @@
+// Matvec kernels for XNQ_Q5K weights (instantiations of k_matvec_impl.h).
+#include "k_matvec_impl.h"
+
+namespace xnq {
+
+hipError_t launch_matvec_q5k(const WView& w, const AView& a, const float* x, size_t m, float* y, hipStream_t s,
+                            bool fused) {
+    return mv::launch_dtype<XNQ_Q5K>(w, a, x, m, y, s, fused);
+}
+
+hipError_t launch_group_q5k(const WGroup& g, const float* x, bool gate, hipStream_t s) {
+    return launch_group_dt<XNQ_Q5K>(g, x, gate, s);
+}
+
+}  // namespace xnq

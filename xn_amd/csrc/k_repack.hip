@@ -212,6 +212,128 @@ __global__ void dequant_kernel(WView w, float* __restrict__ y, size_t total) {
     }
 }
 
+// ---- the padded-block types (Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K) ----
+
+// Where the padded block's bytes come from: bytes [0, a) are GGUF bytes
+// [0, a), bytes [a, a + h) are zero, byte i >= a + h is GGUF byte i - h, and
+// bytes past the GGUF block are zero. Q5_0 inserts 2 zero bytes after d
+// (a = 2, h = 2); Q3K appends 2 (a = stride, h = 0); the others copy.
+// The map is plain arithmetic on host-computed (a, h): a per-dtype branch
+// chain here was miscompiled by hipcc 7.2 for dtypes above Q3K (the byte
+// index stayed at its entry value), which zeroed every Q5K block past d/dmin.
+struct RawMap {
+    uint32_t a, h, tsz, stride;
+};
+inline RawMap raw_map(uint32_t dt) {
+    const uint32_t tsz = (uint32_t)type_size(dt), stride = raw_stride(dt);
+    return dt == XNQ_Q5_0 ? RawMap{2, 2, tsz, stride} : RawMap{stride, 0, tsz, stride};
+}
+__device__ __forceinline__ int raw_src(const RawMap& r, uint32_t i) {
+    const uint32_t j = i < r.a ? i : i - r.h;
+    return (i >= r.a && i < r.a + r.h) || j >= r.tsz ? -1 : (int)j;
+}
+
+// One thread per (row, block).
+__global__ void pad_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ q, size_t total, RawMap r) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const uint8_t* in = src + t * r.tsz;
+    uint8_t* out = q + t * r.stride;  // rows are nb * stride bytes, blocks back to back
+    for (uint32_t i = 0; i < r.stride; i++) {
+        const int j = raw_src(r, i);
+        out[i] = j < 0 ? 0 : in[j];
+    }
+}
+
+__global__ void unpad_kernel(const uint8_t* __restrict__ q, uint8_t* __restrict__ dst, size_t total, RawMap r) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const uint8_t* in = q + t * r.stride;
+    uint8_t* out = dst + t * r.tsz;
+    for (uint32_t i = 0; i < r.stride; i++) {
+        const int j = raw_src(r, i);
+        if (j >= 0) out[j] = in[i];
+    }
+}
+
+// One thread per chunk of 32 outputs; the f32 operations of to_float
+// (k_quants.rs:379-399, 478-502, 585-609, 1014-1053, 1240-1315, 1682-1721).
+template <uint32_t dt>
+__global__ void dequant_raw_kernel(WView w, float* __restrict__ y, size_t total) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const size_t cpr = w.k / 32;
+    const size_t row = t / cpr, c = t % cpr;
+    float* out = y + row * (size_t)w.k + c * 32;
+    const uint32_t stride = raw_stride(dt);
+    if (!is_kquant(dt)) {
+        const uint8_t* b = w.q + row * w.q_row + c * stride;
+        const float d = f16_bits_to_f32(ld16(b));
+        if (dt == XNQ_Q4_1) {
+            const float m = f16_bits_to_f32(ld16(b + 2));
+            for (int j = 0; j < 16; j++) {
+                out[j] = (float)(b[4 + j] & 0x0F) * d + m;
+                out[j + 16] = (float)(b[4 + j] >> 4) * d + m;
+            }
+            return;
+        }
+        const uint32_t qh = *reinterpret_cast<const uint32_t*>(b + 4);
+        for (int j = 0; j < 16; j++) {
+            const uint32_t x0 = (b[8 + j] & 0x0Fu) | (((qh >> j) << 4) & 0x10u);
+            const uint32_t x1 = (b[8 + j] >> 4) | ((qh >> (j + 12)) & 0x10u);
+            if (dt == XNQ_Q5_0) {
+                out[j] = (float)((int)x0 - 16) * d;
+                out[j + 16] = (float)((int)x1 - 16) * d;
+            } else {
+                const float m = f16_bits_to_f32(ld16(b + 2));
+                out[j] = (float)x0 * d + m;
+                out[j + 16] = (float)x1 * d + m;
+            }
+        }
+        return;
+    }
+    const size_t sb = c / 8;
+    const int j = (int)(c % 8);
+    const uint8_t* b = w.q + row * w.q_row + sb * stride;
+    if (dt == XNQ_Q2K) {
+        const int h = j >> 2, sh = 2 * (j & 3);
+        const float d = f16_bits_to_f32(ld16(b + 80)), mn = f16_bits_to_f32(ld16(b + 82));
+        for (int g = 0; g < 2; g++) {
+            const uint8_t sc = b[2 * j + g];
+            const float dl = d * (float)(sc & 0xF), ml = mn * (float)(sc >> 4);
+            for (int l = 0; l < 16; l++) out[16 * g + l] = dl * (float)((b[16 + 32 * h + 16 * g + l] >> sh) & 3) - ml;
+        }
+        return;
+    }
+    if (dt == XNQ_Q3K) {
+        const int h = j >> 2, sh = 2 * (j & 3);
+        const uint32_t* s3 = reinterpret_cast<const uint32_t*>(b + 96);
+        const float d_all = f16_bits_to_f32(ld16(b + 108));
+        const uint32_t bit = 1u << (4 * h + (j & 3));
+        for (int g = 0; g < 2; g++) {
+            const float dl = d_all * ((float)(int8_t)q3k_scale(s3[0], s3[1], s3[2], 2 * j + g) - 32.0f);
+            for (int l = 16 * g; l < 16 * g + 16; l++) {
+                const int v = (int)((b[32 + 32 * h + l] >> sh) & 3) - ((b[l] & bit) == 0 ? 4 : 0);
+                out[l] = dl * (float)v;
+            }
+        }
+        return;
+    }
+    // Q5K
+    const int i = j >> 1, s = j & 1;
+    const float d = f16_bits_to_f32(ld16(b)), mn = f16_bits_to_f32(ld16(b + 2));
+    const uint32_t* sc = reinterpret_cast<const uint32_t*>(b + 4);
+    int scv, mv;
+    q4k_scale_min(sc[0], sc[1], sc[2], j, scv, mv);
+    const float d1 = d * (float)scv, m1 = mn * (float)mv;
+    const uint32_t u = 1u << (2 * i + s);
+    for (int l = 0; l < 32; l++) {
+        const uint8_t ql = b[48 + 32 * i + l];
+        const float nib = (float)(s ? (ql >> 4) : (ql & 0xF));
+        out[l] = d1 * (nib + ((b[16 + l] & u) ? 16.0f : 0.0f)) - m1;
+    }
+}
+
 inline unsigned blocks_for(size_t total, unsigned threads) {
     return (unsigned)((total + threads - 1) / threads);
 }
@@ -221,7 +343,14 @@ inline unsigned blocks_for(size_t total, unsigned threads) {
 hipError_t launch_repack(const WLayout& L, const void* gguf_dev, void* dst_dev, hipStream_t s) {
     WView w = make_wview(L, dst_dev);
     uint8_t* base = static_cast<uint8_t*>(dst_dev);
-    const bool kq = L.dtype == XNQ_Q4K || L.dtype == XNQ_Q6K;
+    if (is_raw_layout(L.dtype)) {
+        const size_t total = L.n * L.nb;
+        if (total == 0) return hipSuccess;
+        pad_kernel<<<blocks_for(total, 128), 128, 0, s>>>(static_cast<const uint8_t*>(gguf_dev), base + L.off_q, total,
+                                                          raw_map(L.dtype));
+        return hipGetLastError();
+    }
+    const bool kq = is_kquant(L.dtype);
     const size_t total = L.n * L.nb * (kq ? 8 : 1);
     if (total == 0) return hipSuccess;
     repack_kernel<<<blocks_for(total, 256), 256, 0, s>>>(
@@ -234,6 +363,11 @@ hipError_t launch_unrepack(const WLayout& L, const void* src_dev, void* gguf_dev
     WView w = make_wview(L, src_dev);
     const size_t total = L.n * L.nb;
     if (total == 0) return hipSuccess;
+    if (is_raw_layout(L.dtype)) {
+        unpad_kernel<<<blocks_for(total, 128), 128, 0, s>>>(w.q, static_cast<uint8_t*>(gguf_dev), total,
+                                                            raw_map(L.dtype));
+        return hipGetLastError();
+    }
     unrepack_kernel<<<blocks_for(total, 128), 128, 0, s>>>(w, static_cast<uint8_t*>(gguf_dev), total);
     return hipGetLastError();
 }
@@ -242,6 +376,18 @@ hipError_t launch_dequant(const WLayout& L, const void* src_dev, float* y, hipSt
     WView w = make_wview(L, src_dev);
     const size_t total = L.n * (L.k / 32);
     if (total == 0) return hipSuccess;
+    if (is_raw_layout(L.dtype)) {
+        const unsigned g = blocks_for(total, 256);
+        switch (L.dtype) {
+        case XNQ_Q4_1: dequant_raw_kernel<XNQ_Q4_1><<<g, 256, 0, s>>>(w, y, total); break;
+        case XNQ_Q5_0: dequant_raw_kernel<XNQ_Q5_0><<<g, 256, 0, s>>>(w, y, total); break;
+        case XNQ_Q5_1: dequant_raw_kernel<XNQ_Q5_1><<<g, 256, 0, s>>>(w, y, total); break;
+        case XNQ_Q2K: dequant_raw_kernel<XNQ_Q2K><<<g, 256, 0, s>>>(w, y, total); break;
+        case XNQ_Q3K: dequant_raw_kernel<XNQ_Q3K><<<g, 256, 0, s>>>(w, y, total); break;
+        default: dequant_raw_kernel<XNQ_Q5K><<<g, 256, 0, s>>>(w, y, total); break;
+        }
+        return hipGetLastError();
+    }
     dequant_kernel<<<blocks_for(total, 256), 256, 0, s>>>(w, y, total);
     return hipGetLastError();
 }

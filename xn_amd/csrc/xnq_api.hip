@@ -75,7 +75,7 @@ const char* dtype_name(uint32_t dt) {
 }
 
 bool device_dtype(uint32_t dt) {
-    return dt == XNQ_Q4_0 || dt == XNQ_Q8_0 || dt == XNQ_Q4K || dt == XNQ_Q6K;
+    return dt == XNQ_Q4_0 || dt == XNQ_Q8_0 || dt == XNQ_Q4K || dt == XNQ_Q6K || is_raw_layout(dt);
 }
 
 // Validation shared by the weight constructors (mod.rs:262-274 check_shape,
@@ -118,8 +118,15 @@ size_t type_size(uint32_t dt) {
     case XNQ_F32: return 4;
     case XNQ_F16: return 2;
     case XNQ_Q4_0: return 18;
+    case XNQ_Q4_1: return 20;
+    case XNQ_Q5_0: return 22;
+    case XNQ_Q5_1: return 24;
     case XNQ_Q8_0: return 34;
+    case XNQ_Q8_1: return 36;
+    case XNQ_Q2K: return 84;
+    case XNQ_Q3K: return 110;
     case XNQ_Q4K: return 144;
+    case XNQ_Q5K: return 176;
     case XNQ_Q6K: return 210;
     case XNQ_Q8K: return 292;
     }
@@ -131,16 +138,27 @@ size_t block_size(uint32_t dt) {
     case XNQ_F32:
     case XNQ_F16: return 1;
     case XNQ_Q4_0:
-    case XNQ_Q8_0: return 32;
+    case XNQ_Q4_1:
+    case XNQ_Q5_0:
+    case XNQ_Q5_1:
+    case XNQ_Q8_0:
+    case XNQ_Q8_1: return 32;
+    case XNQ_Q2K:
+    case XNQ_Q3K:
     case XNQ_Q4K:
+    case XNQ_Q5K:
     case XNQ_Q6K:
     case XNQ_Q8K: return 256;
     }
     return 0;
 }
 
+// k_quants.rs VecDotType of each weight type.  Q8_1 (Q4_1, Q5_1) keeps the
+// Q8_0 quants and scale; its f16 s is derived from them in the kernels.
 uint32_t vec_dot_type(uint32_t wdt) {
-    return (wdt == XNQ_Q4_0 || wdt == XNQ_Q8_0) ? (uint32_t)XNQ_Q8_0 : (uint32_t)XNQ_Q8K;
+    if (is_kquant(wdt)) return XNQ_Q8K;
+    if (wdt == XNQ_Q4_1 || wdt == XNQ_Q5_1) return XNQ_Q8_1;
+    return XNQ_Q8_0;
 }
 
 bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string* err) {
@@ -162,7 +180,12 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
         // d rows padded to 4 bytes: super-block sb's f16 is half (sb & 1) of dword sb / 2
         L.q_row = L.nb * 128; L.h_row = L.nb * 64; L.s_row = L.nb * 16; L.d_row = ((L.nb + 1) & ~size_t(1)) * 2;
         break;
-    default: *err = "unsupported dtype"; return false;
+    default:
+        if (!is_raw_layout(dtype)) {
+            *err = "unsupported dtype";
+            return false;
+        }
+        L.q_row = L.nb * raw_stride(dtype);
     }
     size_t off = 0;
     L.off_q = off;
@@ -183,7 +206,7 @@ ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k) {
     L.act_dtype = vec_dot_type(weight_dtype);
     L.m = m;
     L.k = k;
-    L.img = act_img((uint32_t)k, L.act_dtype == XNQ_Q8K);
+    L.img = act_img((uint32_t)k, L.act_dtype == XNQ_Q8K);  // Q8_1 uses the Q8_0 image
     L.bytes = align_up(m * L.img.row_bytes);
     return L;
 }
@@ -232,19 +255,22 @@ xnq_status xnq_qtensor_upload(int device, uint32_t dtype, const void* gguf_block
     if (!gguf_blocks_host && n) return fail(XNQ_ERR_INVALID, "null block pointer");
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    // Load time, not the hot path: a plain allocation and a blocking copy of
+    // the (pageable) host bytes, then the repack on `stream`.
     hipStream_t s = (hipStream_t)stream;
     const size_t bytes = n * (k / block_size(dtype)) * type_size(dtype);
     void* tmp = nullptr;
-    hipError_t e = hipMallocAsync(&tmp, bytes ? bytes : kAlign, s);
-    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(upload)");
-    e = hipMemcpyAsync(tmp, gguf_blocks_host, bytes, hipMemcpyHostToDevice, s);
+    hipError_t e = hipMalloc(&tmp, bytes ? bytes : kAlign);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(upload)");
+    e = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = hipMemcpy(tmp, gguf_blocks_host, bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
-        (void)hipFreeAsync(tmp, s);
-        return hip_fail(e, "hipMemcpyAsync(upload)");
+        (void)hipFree(tmp);
+        return hip_fail(e, "hipMemcpy(upload)");
     }
     st = xnq_qtensor_upload_device(device, dtype, tmp, n, k, stream, out);
-    (void)hipFreeAsync(tmp, s);
     e = hipStreamSynchronize(s);
+    (void)hipFree(tmp);
     if (st) return st;
     if (e != hipSuccess) {
         xnq_qtensor_free(*out);
@@ -260,6 +286,10 @@ xnq_status xnq_qtensor_quantize(int device, uint32_t dtype, const float* src_dev
     *out = nullptr;
     xnq_status st = check_weight(dtype, n, k);
     if (st) return st;
+    if (is_raw_layout(dtype))
+        return fail(XNQ_ERR_UNSUPPORTED,
+                    "%s: no device quantizer; quantize on the host (GgmlType::from_float) and upload the blocks",
+                    dtype_name(dtype));
     if (!src_dev && n) return fail(XNQ_ERR_INVALID, "null source pointer");
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
@@ -334,6 +364,12 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
         return fail(XNQ_ERR_INVALID, "matmul_t: mkn (%zu, %zu, %zu) does not match weight [%zu, %zu]",
                     m, k, n, qt->L.n, qt->L.k);
     if (m > 0x7fffffffull) return fail(XNQ_ERR_INVALID, "m too large: %zu", m);
+    // vec_dot_q4_1_q8_1 / q5_0_q8_0 / q5_1_q8_1 take pairs of blocks
+    // (k_quants.rs:323-325, 413-415, 519-521)
+    const uint32_t dt = qt->L.dtype;
+    if ((dt == XNQ_Q4_1 || dt == XNQ_Q5_0 || dt == XNQ_Q5_1) && (k / 32) % 2)
+        return fail(XNQ_ERR_INVALID, "vec_dot_%s_%s: %zu, nb is not divisible by 2",
+                    dt == XNQ_Q4_1 ? "q4_1" : dt == XNQ_Q5_0 ? "q5_0" : "q5_1", dt == XNQ_Q5_0 ? "q8_0" : "q8_1", k);
     return XNQ_OK;
 }
 
@@ -619,16 +655,17 @@ xnq_status xnq_qtensor_raw_data(const xnq_qtensor* qt, void* host_dst, size_t ca
     if (bytes == 0) return XNQ_OK;
     if (!host_dst) return fail(XNQ_ERR_INVALID, "null pointer");
     DeviceGuard g(qt->device);
+    // Not the hot path: plain allocation, the unrepack on `stream`, then a
+    // blocking copy into the (pageable) host buffer.
     hipStream_t s = (hipStream_t)stream;
     void* tmp = nullptr;
-    hipError_t e = hipMallocAsync(&tmp, bytes, s);
-    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(raw_data)");
+    hipError_t e = hipMalloc(&tmp, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(raw_data)");
     e = launch_unrepack(qt->L, qt->buf, tmp, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(host_dst, tmp, bytes, hipMemcpyDeviceToHost, s);
-    (void)hipFreeAsync(tmp, s);
-    hipError_t e2 = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = hipMemcpy(host_dst, tmp, bytes, hipMemcpyDeviceToHost);
+    (void)hipFree(tmp);
     if (e != hipSuccess) return hip_fail(e, "raw_data");
-    if (e2 != hipSuccess) return hip_fail(e2, "hipStreamSynchronize(raw_data)");
     return XNQ_OK;
 }
 
@@ -651,6 +688,8 @@ xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* w
     if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");
     if (m == 0) return XNQ_OK;
     if (!workspace_dev || !out_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    if (is_raw_layout(qt->L.dtype))
+        return fail(XNQ_ERR_UNSUPPORTED, "block_ints covers Q4_0, Q8_0, Q4K and Q6K");
     DeviceGuard g(qt->device);
     const WView w = make_wview(qt->L, qt->buf);
     const AView a = make_aview(act_layout(qt->L.dtype, m, qt->L.k), workspace_dev);

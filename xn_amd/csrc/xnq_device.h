@@ -92,6 +92,20 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+// The 16 six-bit Q3K scales (0..63): byte g of the aux words that
+// k_quants.rs:1252-1258 builds from the 12 packed bytes s0, s1, s2.
+__device__ __forceinline__ int q3k_scale(uint32_t s0, uint32_t s1, uint32_t s2, int g) {
+    const uint32_t K1 = 0x03030303u, K2 = 0x0f0f0f0fu;
+    uint32_t a;
+    switch (g >> 2) {
+    case 0: a = (s0 & K2) | ((s2 & K1) << 4); break;
+    case 1: a = (s1 & K2) | (((s2 >> 2) & K1) << 4); break;
+    case 2: a = ((s0 >> 4) & K2) | (((s2 >> 4) & K1) << 4); break;
+    default: a = ((s1 >> 4) & K2) | (((s2 >> 6) & K1) << 4); break;
+    }
+    return (int)((a >> (8 * (g & 3))) & 0xffu);
+}
+
 // Q6K: the 8 dwords of 6-bit values (0..63) of one chunk.
 __device__ __forceinline__ void q6k_unpack(uint4 ql, uint2 qh, int* b) {
     const uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x03030303u;

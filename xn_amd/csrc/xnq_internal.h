@@ -35,8 +35,25 @@ inline size_t align_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a
 //         h plane [n][nb][8][8]  high 2 bits: dword u, byte p, bits 2g'..2g'+1
 //                                hold element 4*(4u+g')+p of the chunk
 //         s plane [n][nb][16] int8 scales, d plane [n][nb] f16
-// nb = blocks per row (k/32 for Q4_0/Q8_0, k/256 for Q4K/Q6K).
+//   Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K: one q plane [n][nb][stride] of the GGUF
+//         blocks padded to a 4-byte multiple (raw_stride below) so every field
+//         is dword aligned: Q5_0 {d, 2 pad, qh[4], qs[16]}, Q3K 2 tail bytes;
+//         the others are their GGUF bytes unchanged.
+// nb = blocks per row (k/32 for the 32-element types, k/256 for the K types).
 // ---------------------------------------------------------------------------
+
+// Super-block (256-element) types, whose activations are Q8K.
+__host__ __device__ constexpr bool is_kquant(uint32_t dt) {
+    return dt == XNQ_Q2K || dt == XNQ_Q3K || dt == XNQ_Q4K || dt == XNQ_Q5K || dt == XNQ_Q6K;
+}
+// Types kept as padded GGUF blocks in one plane, and their stride in bytes.
+__host__ __device__ constexpr bool is_raw_layout(uint32_t dt) {
+    return dt == XNQ_Q4_1 || dt == XNQ_Q5_0 || dt == XNQ_Q5_1 || dt == XNQ_Q2K || dt == XNQ_Q3K || dt == XNQ_Q5K;
+}
+__host__ __device__ constexpr uint32_t raw_stride(uint32_t dt) {
+    return dt == XNQ_Q4_1 ? 20 : dt == XNQ_Q5_0 ? 24 : dt == XNQ_Q5_1 ? 24 : dt == XNQ_Q2K ? 84
+         : dt == XNQ_Q3K ? 112 : dt == XNQ_Q5K ? 176 : 0;
+}
 struct WLayout {
     uint32_t dtype = 0;
     size_t n = 0, k = 0, nb = 0;

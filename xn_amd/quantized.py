@@ -74,12 +74,20 @@ _BLOCK_SIZE = {
 }
 
 # dtypes with a device implementation
-DEVICE_DTYPES = (GgmlDType.Q4_0, GgmlDType.Q8_0, GgmlDType.Q4K, GgmlDType.Q6K)
+DEVICE_DTYPES = (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0,
+                 GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
+# dtypes the device also quantizes from f32 (QTensor.quantize_f32 / QLinear.from_linear)
+DEVICE_QUANTIZE_DTYPES = (GgmlDType.Q4_0, GgmlDType.Q8_0, GgmlDType.Q4K, GgmlDType.Q6K)
 
 
 def vec_dot_type(dtype: GgmlDType) -> GgmlDType:
-    """Activation block type a weight dtype dots against (k_quants.rs:210,615,1321,1727)."""
-    return GgmlDType.Q8_0 if dtype in (GgmlDType.Q4_0, GgmlDType.Q8_0) else GgmlDType.Q8K
+    """Activation block type a weight dtype dots against (the VecDotType of
+    k_quants.rs:210, 310, 405, 507, 615, 883, 1059, 1321, 1510, 1727)."""
+    if dtype in (GgmlDType.Q4_0, GgmlDType.Q5_0, GgmlDType.Q8_0):
+        return GgmlDType.Q8_0
+    if dtype in (GgmlDType.Q4_1, GgmlDType.Q5_1):
+        return GgmlDType.Q8_1
+    return GgmlDType.Q8K
 
 
 def _stream(device: torch.device) -> int:
@@ -379,8 +387,14 @@ def _backend_q(name: str, dtype: GgmlDType):
 
 
 Q40Hip = _backend_q("Q40Hip", GgmlDType.Q4_0)
+Q41Hip = _backend_q("Q41Hip", GgmlDType.Q4_1)
+Q50Hip = _backend_q("Q50Hip", GgmlDType.Q5_0)
+Q51Hip = _backend_q("Q51Hip", GgmlDType.Q5_1)
 Q80Hip = _backend_q("Q80Hip", GgmlDType.Q8_0)
+Q2kHip = _backend_q("Q2kHip", GgmlDType.Q2K)
+Q3kHip = _backend_q("Q3kHip", GgmlDType.Q3K)
 Q4kHip = _backend_q("Q4kHip", GgmlDType.Q4K)
+Q5kHip = _backend_q("Q5kHip", GgmlDType.Q5K)
 Q6kHip = _backend_q("Q6kHip", GgmlDType.Q6K)
 
 
