@@ -106,9 +106,9 @@ struct Lay {
     static constexpr int kRawSlot = kQSlot + kHSlot;
     static constexpr int kPlanes = 2 * 2 * 2 * kBN * 16;  // digit planes [ks][plane][h][n][16]
     static constexpr int kEDa = 0;                          // f32 [kBM]
-    static constexpr int kESum = kEDa + kBM * 4;            // Q4K [kBM][2][16]
+    static constexpr int kESum = kEDa + kBM * 4;            // Q4K [kBM/32][2][32][16]
     static constexpr int kEHdr = kESum + (kQ4K ? kBM * 32 : 0);  // [kBN][16]
-    static constexpr int kEB = kEHdr + kBN * 16;            // Q4K [kBN][2][16]; Q6K d dword [kBN]
+    static constexpr int kEB = kEHdr + kBN * 16;            // Q4K [kBN/32][2][32][16]; Q6K d dword [kBN]
     static constexpr int kEpi = kEB + (kQ4K ? kBN * 32 : kBN * 4);
     static constexpr int kOffA = 0;
     static constexpr int kOffRaw = kOffA + kRing * kASlot;
@@ -127,12 +127,12 @@ struct Lay {
 // global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
 // holds the LDS address lane 0 writes (lane i writes i * size beyond it).
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds_addr)),
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr),
                  "v"(off), "s"(base)
                  : "memory");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds_addr)),
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr),
                  "v"(off), "s"(base)
                  : "memory");
 }
@@ -194,17 +194,23 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
     const uint32_t sb0 = blockIdx.z * sb_per_split;
     const uint32_t K = w.k, nsb = min(sb_per_split, K / 256 - sb0);
     y += blockIdx.z * split_stride;
-    const ActImg& A = a.A;
     const uint32_t lbase = (uint32_t)(uintptr_t)lds;  // low half of the flat address = LDS offset
     const uint32_t lrow = lane & 31, lgrp = lane >> 5;
 
     // Every DMA instruction is issued by the whole wavefront (the vmcnt
     // bookkeeping counts instructions): lanes past the last row or column
     // re-read the last one, and those outputs are dropped at the store.
-    const uint32_t row_max = m - 1 - m0, col_max = w.n - 1 - n0;
-    auto a_row = [&](uint32_t r) { return min(r, row_max) * A.row_bytes; };  // byte offset of tile row r
-    const uint8_t* a_img = a.img + (size_t)m0 * A.row_bytes;
-    const uint8_t* a_q = a_img + sb0 * 128;  // quants: 8 chunks of 16 bytes per super-block and half
+    const uint32_t col_max = w.n - 1 - n0;
+    // Activations come from the row-tiled image: every DMA instruction reads
+    // 1 KiB (d_a: 256 B) of consecutive bytes, lane i's at i * 16 (i * 4).
+    // 64-row blocks past the last one re-read it (those outputs are dropped).
+    const TileImg& T = a.T;
+    const uint32_t nsb_all = K / 256;
+    auto rblk = [&](uint32_t r64) { return min(m0 / 64 + r64, T.rbs - 1); };  // tile-row block r64 -> image block
+    const uint8_t* t_q = a.tile + (size_t)sb0 * 4 * 4096;  // stage st of block rb at rb * 64K + st * 4096
+    const uint8_t* t_d = a.tile + T.d_off + (size_t)sb0 * 256;
+    const uint8_t* t_s = a.tile + T.s_off + (size_t)sb0 * 2048;
+    const uint32_t lane16 = lane * 16, lane4 = lane * 4;
     auto epi_base = [&](uint32_t sb) -> uint8_t* { return lds + L::kOffEpi + (sb & 1) * L::kEpi; };
 
     v16f accf[kTM][kTN];
@@ -240,8 +246,10 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
             }
         }
         if (kQ4K) {
-            const uint4 bmin = reinterpret_cast<const uint4*>(epi + L::kEB)[nl * 2 + lgrp];
-            const uint4 av = reinterpret_cast<const uint4*>(epi + L::kESum)[(rl + lrow) * 2 + lgrp];
+            // both min-term operands are laid out [32-block][half][32] (16 B
+            // each), so the lane's entry is at lane * 16 past a uniform base
+            const uint4 bmin = reinterpret_cast<const uint4*>(epi + L::kEB)[(wn * 2 + j) * 64 + lane];
+            const uint4 av = reinterpret_cast<const uint4*>(epi + L::kESum)[(wm * 2 + i) * 64 + lane];
             const v8bf a8 = __builtin_bit_cast(v8bf, av);
             const v8bf bh8 = __builtin_bit_cast(v8bf, make_uint4(bmin.x, bmin.y, bmin.x, bmin.y));
             const v8bf bl8 = __builtin_bit_cast(v8bf, make_uint4(bmin.z, bmin.w, bmin.z, bmin.w));
@@ -273,7 +281,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
             if (p < 2) {
                 // activation piece t = 2*wave + p: (ks, h, 64-row block)
                 const uint32_t t = 2 * wave + p, ks = t >> 3, h = (t >> 2) & 1, rb = t & 3;
-                dma16(a_q + h * (K / 2) + ks * 16 + st * 32, a_row(rb * 64 + lane),
+                dma16(t_q + (size_t)rblk(rb) * 64 * K + st * 4096 + (ks * 2 + h) * 1024, lane16,
                       lbase + L::kOffA + slot * L::kASlot + ((ks * 2 + h) * kBM + rb * 64) * 16);
                 return;
             }
@@ -285,10 +293,11 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                 if (!kQ4K && p == kBase + 1)
                     dma4(wd + ((sb0 + sb) & ~1u) * 2, min(col, col_max) * w.d_row, epi + L::kEB + cw * 64 * 4);
             } else {
-                if (p == kBase) dma4(a_img + A.d_off + (sb0 + sb) * 4, a_row(64 * gw + lane), epi + L::kEDa + 64 * gw * 4);
+                if (p == kBase)
+                    dma4(t_d + ((size_t)rblk(gw) * nsb_all + sb) * 256, lane4, epi + L::kEDa + 64 * gw * 4);
                 if (kQ4K && p > kBase) {
-                    const uint32_t i = p - kBase - 1;  // rows 64*gw + 32*i + lane/2
-                    dma16(a_img + A.s_off + (sb0 + sb) * 32, a_row(64 * gw + 32 * i + (lane >> 1)) + (lane & 1) * 16,
+                    const uint32_t i = p - kBase - 1;  // row 64*gw + 32*i + lane%32, half lane/32
+                    dma16(t_s + (((size_t)rblk(gw) * nsb_all + sb) * 2 + i) * 1024, lane16,
                           epi + L::kESum + (64 * gw + 32 * i) * 32);
                 }
             }
@@ -308,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                     for (int i = 0; i < 2; i++) {
                         uint4* sp = reinterpret_cast<uint4*>(epi + L::kESum + (64 * gw + 32 * i) * 32) + lane;
                         const uint4 pr = *sp;
-                        const float da = eda[64 * gw + 32 * i + (lane >> 1)];
+                        const float da = eda[64 * gw + 32 * i + (lane & 31)];
                         const uint32_t prs[4] = {pr.x, pr.y, pr.z, pr.w};
                         float v[4];
 #pragma unroll
@@ -349,7 +358,8 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                         q4k_scale_min(hd.y, hd.z, hd.w, (int)(4 * bc + t), sc2, mn2);
                         v[t] = dm * (float)mn2;
                     }
-                    *reinterpret_cast<uint4*>(epi + L::kEB + (col * 2 + bc) * 16) = bf16_split4(v);
+                    *reinterpret_cast<uint4*>(epi + L::kEB + (((cw * 2 + (lane >> 5)) * 2 + bc) * 32 + (lane & 31)) * 16) =
+                        bf16_split4(v);
                 }
             } else {
                 const uint2 qh = *reinterpret_cast<const uint2*>(raw + L::kQSlot + (bc * kBN + col) * 16 + bc * 8);
@@ -548,6 +558,8 @@ uint32_t mfma_splits(size_t m, size_t n, size_t k) {
 hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                        hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
+    // the kernel reads the row-tiled activation image, which must cover m rows
+    if (!a.tile || (size_t)a.T.rbs * 64 < m || a.k != w.k) return hipErrorInvalidValue;
     if (splits > 1 && !partial) splits = 1;
     if (w.dtype == XNQ_Q4K) return launch_dt<XNQ_Q4K>(w, a, m, splits, y, partial, s);
     if (w.dtype == XNQ_Q6K) return launch_dt<XNQ_Q6K>(w, a, m, splits, y, partial, s);

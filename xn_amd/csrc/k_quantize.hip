@@ -23,7 +23,8 @@ constexpr int kWave = 64;
 template <bool CANONICAL>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
                                                             size_t nblocks, ActImg A,
-                                                            uint8_t* __restrict__ out) {
+                                                            uint8_t* __restrict__ out,
+                                                            uint8_t* __restrict__ tile, TileImg T) {
     const int lane = threadIdx.x & (kWave - 1);
     const size_t blk = (size_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
     if (blk >= nblocks) return;  // uniform over the wavefront
@@ -37,7 +38,23 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
         if ((lane & 3) == 0) reinterpret_cast<int16_t*>(b + 260)[lane >> 2] = (int16_t)r.bsum;
     } else {
         const size_t bpr = A.k / 256;
-        q8k_store(out + (blk / bpr) * A.row_bytes, A, (uint32_t)(blk % bpr), lane, r);
+        const size_t row = blk / bpr, sb = blk % bpr;
+        q8k_store(out + row * A.row_bytes, A, (uint32_t)sb, lane, r);
+        if (tile) {
+            // lane's elements 4*lane .. 4*lane+3 of super-block sb: chunk
+            // 8*sb + lane/8 = stage 4*sb + lane/16, ks = (lane/8)&1, half (lane/4)&1
+            const size_t rb = row >> 6, r64 = row & 63;
+            const size_t st = 4 * sb + (lane >> 4), piece = (lane >> 2) & 3;  // ks * 2 + h
+            *reinterpret_cast<uint32_t*>(tile + rb * 64 * A.k + st * 4096 + piece * 1024 + r64 * 16 +
+                                         4 * (lane & 3)) = r.packed;
+            const size_t rs = rb * bpr + sb;
+            if (lane == 0) reinterpret_cast<float*>(tile + T.d_off + rs * 256)[r64] = r.d;
+            if ((lane & 3) == 0) {
+                const int g = lane >> 2;  // bsum group 0..15
+                reinterpret_cast<int16_t*>(tile + T.s_off + (rs * 2 + (r64 >> 5)) * 1024 + (g >> 3) * 512 +
+                                           (r64 & 31) * 16)[g & 7] = (int16_t)r.bsum;
+            }
+        }
     }
 }
 
@@ -374,7 +391,8 @@ hipError_t launch_quantize_act(const ALayout& L, const float* x, void* ws, hipSt
     if (L.m == 0) return hipSuccess;
     if (L.act_dtype == XNQ_Q8K) {
         const size_t nblocks = L.m * (L.k / 256);
-        quantize_q8k_kernel<false><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, L.img, b);
+        quantize_q8k_kernel<false><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(
+            x, nblocks, L.img, b, L.tiled ? b + L.tile_off : nullptr, L.tile);
     } else {
         const size_t nblocks = L.m * (L.k / 32);
         quantize_q80_kernel<false><<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, nblocks, L.img, b);
@@ -389,7 +407,7 @@ hipError_t launch_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, co
     const ActImg A = act_img((uint32_t)k, act_dtype == XNQ_Q8K);
     if (act_dtype == XNQ_Q8K) {
         const size_t nblocks = m * (k / 256);
-        quantize_q8k_kernel<true><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, A, b);
+        quantize_q8k_kernel<true><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, A, b, nullptr, TileImg{});
     } else {
         const size_t nblocks = m * (k / 32);
         quantize_q80_kernel<true><<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, nblocks, A, b);

@@ -80,12 +80,12 @@ struct KLay {
 // global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
 // holds the LDS address lane 0 writes (lane i writes i * size beyond it).
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds_addr)),
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr),
                  "v"(off), "s"(base)
                  : "memory");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds_addr)),
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr),
                  "v"(off), "s"(base)
                  : "memory");
 }

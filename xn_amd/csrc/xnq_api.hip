@@ -201,6 +201,26 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
     return true;
 }
 
+static size_t env_size(const char* name, size_t dflt) {
+    const char* e = getenv(name);
+    return e ? (size_t)strtoull(e, nullptr, 10) : dflt;
+}
+
+size_t skinny_max_rows() {
+    static const size_t v = env_size("XNQ_SKINNY_MAX_ROWS", 64);
+    return v;
+}
+
+// Whether the prefill (tiled MFMA) route can be taken for m activation rows,
+// in which case the activation quantizer also writes the row-tiled image.
+// It depends on m and the forced route, not on n, so xnq_quantize_lhs (which
+// has no n) and the matmul agree; xnq_set_route must not change between them.
+bool tiled_act(uint32_t weight_dtype, size_t m, size_t k) {
+    const int forced = g_route.load();
+    if (forced == 1 || forced == 3) return false;
+    return mfma_supported(weight_dtype, m, 0, k) && (forced == 2 || m > skinny_max_rows());
+}
+
 ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k) {
     ALayout L;
     L.act_dtype = vec_dot_type(weight_dtype);
@@ -208,6 +228,12 @@ ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k) {
     L.k = k;
     L.img = act_img((uint32_t)k, L.act_dtype == XNQ_Q8K);  // Q8_1 uses the Q8_0 image
     L.bytes = align_up(m * L.img.row_bytes);
+    if (tiled_act(weight_dtype, m, k)) {
+        L.tiled = true;
+        L.tile_off = L.bytes;
+        L.tile = tile_img(m, (uint32_t)k);
+        L.bytes = align_up(L.tile_off + L.tile.bytes);
+    }
     return L;
 }
 
@@ -382,14 +408,9 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
 // XNQ_MFMA_MIN_ROWS override the crossovers for tuning.
 enum Route { kMatvec, kSkinny, kMfma };
 
-static size_t env_size(const char* name, size_t dflt) {
-    const char* e = getenv(name);
-    return e ? (size_t)strtoull(e, nullptr, 10) : dflt;
-}
-
 static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k) {
     static const size_t skinny_min = env_size("XNQ_SKINNY_MIN_ROWS", 0);
-    static const size_t skinny_max = env_size("XNQ_SKINNY_MAX_ROWS", 64);
+    const size_t skinny_max = skinny_max_rows();
     const int forced = g_route.load();
     if (forced == 1) return kMatvec;
     if (forced == 2) return kMfma;

@@ -101,16 +101,43 @@ __host__ __device__ inline uint32_t act_q_off(uint32_t k, uint32_t e) {
     return (o >> 4) * (k / 2) + c * 16 + (o & 15);
 }
 
+// Row-tiled copy of a Q8K image, written beside it when the prefill kernel
+// may read it: rows in blocks of 64 (the last block padded), and within a
+// block every piece one DMA instruction of the prefill kernel fetches is
+// 1 KiB (or 256 B) of consecutive bytes, lane i's 16 (or 4) at i * 16 (i * 4):
+//   quants  [rb][stage = 64 K][ks][h][row 64][16]: chunk 2*stage+ks, bytes 16h..16h+15
+//   d       [rb][sb][row 64] f32
+//   bsums   [rb][sb][row / 32][half][row % 32][16]: int16 bsums 8*half..8*half+7
+struct TileImg {
+    uint32_t rbs = 0;  // 64-row blocks
+    size_t d_off = 0, s_off = 0, bytes = 0;
+};
+
+__host__ __device__ inline TileImg tile_img(size_t m, uint32_t k) {
+    TileImg T;
+    T.rbs = (uint32_t)((m + 63) / 64);
+    const size_t nsb = k / 256;
+    T.d_off = (size_t)T.rbs * 64 * k;
+    T.s_off = T.d_off + (size_t)T.rbs * nsb * 256;
+    T.bytes = T.s_off + (size_t)T.rbs * nsb * 2048;
+    return T;
+}
+
 struct ALayout {
     uint32_t act_dtype = 0;
     size_t m = 0, k = 0, bytes = 0;
     ActImg img{};
+    bool tiled = false;  // a TileImg follows the row images at tile_off
+    size_t tile_off = 0;
+    TileImg tile{};
 };
 
 struct AView {
     const uint8_t* img;
     uint32_t m, k;
     ActImg A;
+    const uint8_t* tile;  // null unless the layout is tiled
+    TileImg T;
 };
 
 // Weights that share one activation row in a decode launch (matvec
@@ -156,6 +183,8 @@ inline AView make_aview(const ALayout& L, const void* base) {
     v.m = (uint32_t)L.m;
     v.k = (uint32_t)L.k;
     v.A = L.img;
+    v.tile = L.tiled ? v.img + L.tile_off : nullptr;
+    v.T = L.tile;
     return v;
 }
 
