@@ -35,6 +35,11 @@
 // for its own DMA (s_waitcnt vmcnt with the exact count of younger DMA it has
 // issued) and processes only data it fetched itself, so one barrier per stage
 // publishes both the next activation tile and the next digit planes.
+//
+// Activations come from the row-tiled copy of the Q8K image (TileImg), in
+// which every activation DMA instruction reads 1 KiB of consecutive bytes:
+// reading the row images directly costs one cache line per lane (64 per
+// instruction), which measured a quarter of the kernel's time at M = 512.
 #include <type_traits>
 
 #include "xnq_device.h"
