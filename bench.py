@@ -367,7 +367,7 @@ def main():
         ms_kern = time_graph(g_kern, stream) / args.steps
         ms_split = time_graph(g_split, stream) / args.steps
         result["matvec_variants_us"] = {
-            "fused_step": round(ms_step * 1e3, 3),
+            "matmul_t_step": round(ms_step * 1e3, 3),
             "preq_kernel": round(ms_kern * 1e3, 3),
             "quantize_then_preq_step": round(ms_split * 1e3, 3),
         }

@@ -475,11 +475,22 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     return XNQ_OK;
 }
 
-// Decode: the matvec route for up to 8 rows quantizes the activation rows in
-// LDS inside the matvec kernels and needs no workspace.
+// Decode: the fused matvec route for up to 8 rows quantizes the activation
+// rows in LDS inside the matvec kernels and needs no workspace.  The fused kernels (quantize in LDS, then stream) save the quantize launch
+// but stream the weights more slowly than the plain matvec kernel, by an
+// amount that grows with n (measured at m = 1: +0.7 us at 4096 x 4096,
+// +4.7 us at 4096 -> 14336, +17 us at 8192 -> 28672, against ~1.8 us for the
+// separate quantize launch), so they take small weights only.
+static size_t fused_max_rows() {
+    static const size_t v = env_size("XNQ_FUSED_MAX_ROWS", 6144);
+    return v;
+}
+
 static bool fused_route(const xnq_qtensor* qt, size_t m) {
     const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k);
-    return r == kMatvec && (m <= 8 || g_route.load() == 1);
+    if (r != kMatvec) return false;
+    if (g_route.load() == 1) return true;
+    return m <= 8 && qt->L.n <= fused_max_rows();
 }
 
 size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m) {

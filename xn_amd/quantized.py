@@ -263,7 +263,7 @@ class QTensor:
     def matmul_t(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
         """dst[m, n] = quantize(lhs[m, k]) . W^T (mod.rs:334-339, k_quants.rs:1996-2011).
 
-        Decode-sized m (the matvec route) is one kernel that quantizes the
+        Decode-sized m on small weights is one kernel that quantizes the
         rows in LDS; otherwise the quantized activation goes to a workspace
         from torch's caching allocator (graph-capture safe, no per-call
         device allocation) and the library runs quantize_lhs + T::matmul, as
