@@ -475,14 +475,15 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     return XNQ_OK;
 }
 
-// Decode: the fused matvec route for up to 8 rows quantizes the activation
-// rows in LDS inside the matvec kernels and needs no workspace.  The fused kernels (quantize in LDS, then stream) save the quantize launch
-// but stream the weights more slowly than the plain matvec kernel, by an
-// amount that grows with n (measured at m = 1: +0.7 us at 4096 x 4096,
-// +4.7 us at 4096 -> 14336, +17 us at 8192 -> 28672, against ~1.8 us for the
-// separate quantize launch), so they take small weights only.
-static size_t fused_max_rows() {
-    static const size_t v = env_size("XNQ_FUSED_MAX_ROWS", 6144);
+// Decode: the fused matvec route quantizes the activation row in LDS inside
+// the matvec kernel and needs no workspace.  It saves the quantize launch
+// (~1.8 us) but streams the weights more slowly than the plain matvec kernel,
+// by an amount that grows with the weight (measured at m = 1: +0.7 us at
+// 4096 x 4096, +4.7 us at 4096 -> 14336, +17 us at 8192 -> 28672) and with m
+// (m = 2, 14336 -> 4096: 23 us against 11 + 1.8), so it takes m = 1 on
+// weights of up to XNQ_FUSED_MAX_ELEMS (6144 x 4096) elements only.
+static size_t fused_max_elems() {
+    static const size_t v = env_size("XNQ_FUSED_MAX_ELEMS", (size_t)6144 * 4096);
     return v;
 }
 
@@ -490,7 +491,7 @@ static bool fused_route(const xnq_qtensor* qt, size_t m) {
     const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k);
     if (r != kMatvec) return false;
     if (g_route.load() == 1) return true;
-    return m <= 8 && qt->L.n <= fused_max_rows();
+    return m == 1 && qt->L.n * qt->L.k <= fused_max_elems();
 }
 
 size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m) {
