@@ -111,8 +111,9 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
 
 /* matmul_t with caller-owned scratch (no allocation inside): workspace_dev
  * holds at least xnq_qtensor_matmul_t_workspace_size(qt, m) bytes, which is
- * 0 on the decode route (m <= 8 rows quantized in LDS by the matvec kernels;
- * workspace_dev may then be NULL).  Same contract as xnq_qtensor_matmul_t
+ * 0 on the fused decode route (m == 1 on weights of up to 6144 x 4096
+ * elements, the row quantized in LDS by the matvec kernel; workspace_dev may
+ * then be NULL).  Same contract as xnq_qtensor_matmul_t
  * (QTensor::matmul_t, mod.rs:334-339; k_quants::matmul, k_quants.rs:1996-2011). */
 size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m);
 xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
@@ -126,12 +127,12 @@ xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, si
  * silu_gate: dst[m x n] = silu(lhs . gate^T) * (lhs . up^T), the SwiGLU of
  * llama.rs:258-264 (Mlp::forward) with silu(s) = s / (1 + exp(0 - s))
  * (cpu_backend.rs:354-356); gate and up have one shape.  m == 1 with both on
- * the decode route and K <= 10240 is one kernel and needs no workspace;
+ * the fused decode route and K <= 10240 is one kernel and needs no workspace;
  * otherwise the two products go through matmul_t_ws and a SiLU-multiply
  * kernel, with workspace for the second product.
  *
  * group: dsts[i][m x n_i] = lhs . qts[i]^T for up to 3 weights of one dtype
- * and K (the q, k, v projections of llama.rs:156-158); m == 1 on the decode
+ * and K (the q, k, v projections of llama.rs:156-158); m == 1 on the fused decode
  * route is one kernel over the joined rows, other cases one matmul_t_ws per
  * weight.  Workspace sizes are 0 when the single-kernel route applies. */
 size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m);
@@ -197,7 +198,7 @@ xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* w
  * not run; xnq_graph_launch replays it with the same device pointers.  Inside
  * a capture use the entry points that allocate nothing: matmul_t_ws,
  * quantize_lhs + matmul_preq, silu_gate / group with their workspaces, and
- * matmul_t on the decode route (m <= 8); matmul_t fails with XNQ_ERR_INVALID
+ * matmul_t on the fused decode route; matmul_t fails with XNQ_ERR_INVALID
  * where it would allocate.  A failed capture is discarded with
  * xnq_capture_abort. */
 typedef struct xnq_graph xnq_graph;

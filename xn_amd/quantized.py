@@ -279,7 +279,7 @@ class QTensor:
                                         _ptr(dst), _stream(self.device)))
 
     def matmul_t_workspace_size(self, m: int) -> int:
-        """Bytes of caller scratch matmul_t_ws needs for m rows (0 on the decode route)."""
+        """Bytes of caller scratch matmul_t_ws needs for m rows (0 on the fused decode route)."""
         return int(_lib.load().xnq_qtensor_matmul_t_workspace_size(self.storage.handle, int(m)))
 
     def matmul_t_ws(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, ws: Optional[torch.Tensor],
@@ -312,8 +312,8 @@ class QTensor:
 
     def matmul_t_abi(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
         """The same product through the single C entry point xnq_qtensor_matmul_t
-        (what a foreign caller binds): m <= 8 quantizes inside the matvec
-        kernels, larger m uses a stream-ordered workspace."""
+        (what a foreign caller binds): m == 1 on small weights quantizes inside
+        the matvec kernel, other calls use a stream-ordered workspace."""
         m, k, n = self._check_mm(mkn, lhs, dst)
         check(_lib.load().xnq_qtensor_matmul_t(self.storage.handle, m, k, n, _ptr(lhs), _ptr(dst),
                                                _stream(self.device)))
