@@ -184,10 +184,14 @@ xnq_status xnq_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const
 
 /* Integer parts of every per-block dot product the matvec kernel forms, for
  * bit-exactness checks against the CPU vec_dot (k_quants.rs:287-304,
- * 677-691, 1337-1416, 1743-1798).  workspace_dev comes from
- * xnq_quantize_lhs.  out_dev receives int32 [m][n][k/256 or k/32][2]:
- *   Q4_0, Q8_0: [block integer sum, 0]
- *   Q4K:        [sum_j sc_j * sum q4*q8, sum_j m_j * bsum_j]
+ * 316-343, 419-440, 513-544, 677-691, 899-948, 1071-1152, 1337-1416,
+ * 1524-1605, 1743-1798).  workspace_dev comes from xnq_quantize_lhs.
+ * out_dev receives int32 [m][n][k/256 or k/32][2]:
+ *   Q4_0, Q8_0, Q4_1, Q5_1: [block integer sum, 0]
+ *   Q5_0:       [sum (q5-16)*q8, 0]
+ *   Q2K:        [sum_g (sc_g & 15) * sum q2*q8, sum_g (sc_g >> 4) * bsum_g]
+ *   Q3K:        [sum_g (sc_g - 32) * sum q3*q8, 0]   (q3 in -4..3)
+ *   Q4K, Q5K:   [sum_j sc_j * sum q*q8, sum_j m_j * bsum_j]
  *   Q6K:        [sum_j sc_j * sum (q6-32)*q8, 0] */
 xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* workspace_dev,
                                   int32_t* out_dev, void* stream);

@@ -142,7 +142,43 @@ def decode_q6k(blocks: np.ndarray):
 
 # ------------------------------------------------- brute-force integer dots
 def block_ints_bruteforce(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: int, k: int):
-    """int64 [m, n, nb, 2] from decoded integers (see xnq.h block_ints)."""
+    """int64 [m, n, nb, 2] from decoded integers (see xnq.h block_ints).
+
+    a_blocks are the weight type's vec-dot blocks: Q8_0 for Q4_0, Q8_0 and
+    Q5_0, Q8_1 for Q4_1 and Q5_1, Q8_K for the K types."""
+    if dt in (3, 6, 7):  # Q4_1, Q5_0, Q5_1: [sum q*a, 0] per 32-block
+        nb = k // 32
+        qa = (decode_q8_0(a_blocks)[1] if dt == 6 else decode_q8_1(a_blocks)[2]).reshape(m, nb, 32)
+        qw = {3: lambda b: decode_q4_1(b)[2], 6: lambda b: decode_q5_0(b)[1],
+              7: lambda b: decode_q5_1(b)[2]}[dt](w_blocks).reshape(n, nb, 32)
+        out = np.zeros((m, n, nb, 2), np.int64)
+        out[..., 0] = np.einsum("mbe,nbe->mnb", qa, qw)
+        return out
+    if dt in (10, 11, 13):  # Q2K, Q3K, Q5K
+        nb = k // 256
+        _, qa, bsums = decode_q8k(a_blocks)
+        qa = qa.reshape(m, nb, 256)
+        bsums = bsums.reshape(m, nb, 16)
+        out = np.zeros((m, n, nb, 2), np.int64)
+        if dt == 10:
+            _, _, sc, mn, q = decode_q2k(w_blocks)
+            sc, mn, q = sc.reshape(n, nb, 16), mn.reshape(n, nb, 16), q.reshape(n, nb, 16, 16)
+            sub = np.einsum("mbge,nbge->mnbg", qa.reshape(m, nb, 16, 16), q)
+            out[..., 0] = np.einsum("mnbg,nbg->mnb", sub, sc)
+            out[..., 1] = np.einsum("mbg,nbg->mnb", bsums, mn)
+        elif dt == 11:
+            _, sc, q = decode_q3k(w_blocks)
+            sc, q = sc.reshape(n, nb, 16), q.reshape(n, nb, 16, 16)
+            sub = np.einsum("mbge,nbge->mnbg", qa.reshape(m, nb, 16, 16), q)
+            out[..., 0] = np.einsum("mnbg,nbg->mnb", sub, sc)
+        else:
+            _, _, sc, mn, q = decode_q5k(w_blocks)
+            sc, mn, q = sc.reshape(n, nb, 8), mn.reshape(n, nb, 8), q.reshape(n, nb, 8, 32)
+            sub = np.einsum("mbje,nbje->mnbj", qa.reshape(m, nb, 8, 32), q)
+            out[..., 0] = np.einsum("mnbj,nbj->mnb", sub, sc)
+            s32 = bsums.reshape(m, nb, 8, 2).sum(axis=3)
+            out[..., 1] = np.einsum("mbj,nbj->mnb", s32, mn)
+        return out
     if dt in (2, 8):
         nb = k // 32
         da, qa = decode_q8_0(a_blocks)

@@ -1,12 +1,14 @@
 """GPU parity for the remaining GGUF dtypes (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K,
 Q5_K; mod.rs:444-455 supports them on the CPU), through the C ABI, against
-the CPU oracle (oracle/xnq_oracle_more.c): raw_data round trips and
-dequantization bit-exact, matmul outputs within the path's f32 tolerance.
+the CPU oracle (oracle/xnq_oracle_more.c): raw_data round trips,
+dequantization and the integer parts of every block dot bit-exact, matmul
+outputs within the path's f32 tolerance.
 """
 import numpy as np
 import pytest
 import torch
 
+from tests import _formats as F
 from tests.test_gpu_parity import assert_close, upload
 
 pytestmark = pytest.mark.gpu
@@ -37,6 +39,25 @@ def test_dequantize_bit_exact(orc, dev, dt):
     got = upload(blocks, n, k, dt, dev).dequantize().cpu().numpy().reshape(-1)
     want = orc.to_float(dt, blocks)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt", MORE)
+def test_block_ints_bit_exact(orc, dev, dt):
+    """The integer parts of every block dot the matvec kernels scale equal the
+    ones brute-forced from independently decoded quants (k_quants.rs:316-343,
+    419-440, 513-544, 899-948, 1071-1152, 1524-1605)."""
+    from xn_amd.quantized import block_ints, lhs_workspace, quantize_lhs
+
+    rng = np.random.default_rng(9300 + dt)
+    m, n, k = 3, 21, 1024
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    ws = lhs_workspace(qt.dtype(), m, k, dev)
+    quantize_lhs(qt.dtype(), torch.from_numpy(x).to(dev), ws, m, k)
+    got = block_ints(qt, m, ws).cpu().numpy().astype(np.int64)
+    want = F.block_ints_bruteforce(dt, blocks, orc.quantize_lhs(dt, x), m, n, k)
+    assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize("dt", MORE)

@@ -168,41 +168,13 @@ def test_make_q3_quants_degenerate_and_grid(orc):
     assert np.allclose((ls.astype(np.float32) - 4) * s, x, atol=1e-6)
 
 
-def _brute(dt, w, a, m, n, k):
-    """int64 [m, n, nb, 2] of the K-type block dots from independently decoded integers."""
-    nb = k // 256
-    _, qa, bsums = F.decode_q8k(a)
-    qa = qa.reshape(m, nb, 256)
-    bsums = bsums.reshape(m, nb, 16)
-    out = np.zeros((m, n, nb, 2), np.int64)
-    if dt == Q2K:
-        _, _, sc, mn, q = F.decode_q2k(w)
-        sc, mn, q = sc.reshape(n, nb, 16), mn.reshape(n, nb, 16), q.reshape(n, nb, 16, 16)
-        sub = np.einsum("mbge,nbge->mnbg", qa.reshape(m, nb, 16, 16), q)
-        out[..., 0] = np.einsum("mnbg,nbg->mnb", sub, sc)
-        out[..., 1] = np.einsum("mbg,nbg->mnb", bsums, mn)
-    elif dt == Q3K:
-        _, sc, q = F.decode_q3k(w)
-        sc, q = sc.reshape(n, nb, 16), q.reshape(n, nb, 16, 16)
-        sub = np.einsum("mbge,nbge->mnbg", qa.reshape(m, nb, 16, 16), q)
-        out[..., 0] = np.einsum("mnbg,nbg->mnb", sub, sc)
-    else:
-        _, _, sc, mn, q = F.decode_q5k(w)
-        sc, mn, q = sc.reshape(n, nb, 8), mn.reshape(n, nb, 8), q.reshape(n, nb, 8, 32)
-        sub = np.einsum("mbje,nbje->mnbj", qa.reshape(m, nb, 8, 32), q)
-        out[..., 0] = np.einsum("mnbj,nbj->mnb", sub, sc)
-        s32 = bsums.reshape(m, nb, 8, 2).sum(axis=3)
-        out[..., 1] = np.einsum("mbj,nbj->mnb", s32, mn)
-    return out
-
-
 @pytest.mark.parametrize("dt", [Q2K, Q3K, Q5K])
 def test_kquant_block_ints_bruteforce(orc, dt):
     rng = np.random.default_rng(140 + dt)
     m, n, k = 3, 5, 512
     w = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
     a = orc.quantize_lhs(dt, rng.normal(0, 1, (m, k)))
-    assert np.array_equal(orc.block_ints(dt, w, a, m, n, k), _brute(dt, w, a, m, n, k))
+    assert np.array_equal(orc.block_ints(dt, w, a, m, n, k), F.block_ints_bruteforce(dt, w, a, m, n, k))
 
 
 @pytest.mark.parametrize("dt", [Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K])

@@ -1,5 +1,5 @@
 // Dispatch of the matvec kernels (k_matvec_impl.h, instantiated per dtype in
-// k_matvec_<dtype>.hip) and the block-integer kernel used by exactness tests.
+// k_matvec_<dtype>.hip) and the block-integer kernels used by exactness tests.
 // The integer part of every block dot is exact; only the final f32 combine
 // differs in rounding order from xn's vec_dot (k_quants.rs:287-304, 677-691,
 // 1337-1416, 1743-1798).
@@ -52,6 +52,38 @@ __global__ void block_ints_kernel(WView w, AView a, uint32_t m, int32_t* __restr
             r0 += q6k_chunk_int(ql, qh, av, sc[2 * j], sc[2 * j + 1], (int)(int16_t)(sv & 0xffff),
                                 (int)(int16_t)(sv >> 16));
         }
+    }
+    out[2 * t] = r0;
+    out[2 * t + 1] = r1;
+}
+
+// The same for the padded-block types: one thread per (activation row,
+// weight row, block), the block's chunks through load_chunk / chunk_ints, so
+// the integers are the ones the matvec kernels scale.
+template <int DT>
+__global__ void block_ints_raw_kernel(WView w, AView a, uint32_t m, int32_t* __restrict__ out) {
+    constexpr uint32_t kChunks = is_kquant(DT) ? 8 : 1;
+    const uint32_t nb = w.nb;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)m * w.n * nb;
+    if (t >= total) return;
+    const uint32_t b = (uint32_t)(t % nb);
+    const uint32_t row = (uint32_t)((t / nb) % w.n);
+    const uint32_t mr = (uint32_t)(t / ((size_t)nb * w.n));
+    const uint8_t* img = a.img + (size_t)mr * a.A.row_bytes;
+    const int32_t* sums = reinterpret_cast<const int32_t*>(img + a.A.s_off);
+    int32_t r0 = 0, r1 = 0;
+    for (uint32_t c = b * kChunks; c < b * kChunks + kChunks; c++) {
+        const uint4 lo4 = *reinterpret_cast<const uint4*>(img + c * 16);
+        const uint4 hi4 = *reinterpret_cast<const uint4*>(img + w.k / 2 + c * 16);
+        const int av[8] = {(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
+                           (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
+        mv::Chunk ch;
+        mv::load_chunk<DT>(w, row, c, ch);
+        int i0, i1;
+        mv::chunk_ints<DT>(ch, c, av, sums[c], i0, i1);
+        r0 += i0;
+        r1 += i1;
     }
     out[2 * t] = r0;
     out[2 * t + 1] = r1;
@@ -127,9 +159,17 @@ hipError_t launch_matvec_group(const WGroup& g, const float* x, bool gate, hipSt
 }
 
 hipError_t launch_block_ints(const WView& w, const AView& a, size_t m, int32_t* out, hipStream_t s) {
-    if (is_raw_layout(w.dtype)) return hipErrorNotSupported;
     const size_t total = m * w.n * w.nb;
     if (total == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((total + 127) / 128);
+    switch (w.dtype) {
+    case XNQ_Q4_1: block_ints_raw_kernel<XNQ_Q4_1><<<grid, 128, 0, s>>>(w, a, (uint32_t)m, out); return hipGetLastError();
+    case XNQ_Q5_0: block_ints_raw_kernel<XNQ_Q5_0><<<grid, 128, 0, s>>>(w, a, (uint32_t)m, out); return hipGetLastError();
+    case XNQ_Q5_1: block_ints_raw_kernel<XNQ_Q5_1><<<grid, 128, 0, s>>>(w, a, (uint32_t)m, out); return hipGetLastError();
+    case XNQ_Q2K: block_ints_raw_kernel<XNQ_Q2K><<<grid, 128, 0, s>>>(w, a, (uint32_t)m, out); return hipGetLastError();
+    case XNQ_Q3K: block_ints_raw_kernel<XNQ_Q3K><<<grid, 128, 0, s>>>(w, a, (uint32_t)m, out); return hipGetLastError();
+    case XNQ_Q5K: block_ints_raw_kernel<XNQ_Q5K><<<grid, 128, 0, s>>>(w, a, (uint32_t)m, out); return hipGetLastError();
+    }
     block_ints_kernel<<<(unsigned)((total + 127) / 128), 128, 0, s>>>(w, a, (uint32_t)m, out);
     return hipGetLastError();
 }

@@ -235,10 +235,82 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x, int w) {
     return (v & 1u) | ((v & 2u) << 7) | ((v & 4u) << 14) | ((v & 8u) << 21);
 }
 
-// f32 combine of one weight chunk c against one activation chunk: a[8] the
-// 32 int8 (elements 0-15 in a[0..3], 16-31 in a[4..7]), sv the chunk's side
-// word (Q8K: bsum of elements 0-15 | bsum of 16-31 << 16; Q8_0: the block
-// sum), da the activation block scale.  Integer parts are exact; the f32
+// Integer parts of one chunk's dot for the padded-block types: a[8] the
+// chunk's 32 int8 activations (elements 0-15 in a[0..3], 16-31 in a[4..7]),
+// sv the chunk's side word (Q8K: bsum of elements 0-15 | bsum of 16-31 << 16;
+// Q8_0: the block sum):
+//   Q4_1, Q5_1: r0 = sum q*a;  Q5_0: r0 = sum (q - 16)*a;  r1 = 0
+//   Q2K: r0 = sum_g (sc_g & 15) * sum q2*a,  r1 = sum_g (sc_g >> 4) * bsum_g
+//   Q3K: r0 = sum_g (sc_g - 32) * sum (q3 - 4 * !hbit)*a,  r1 = 0
+//   Q5K: r0 = sc_j * sum q5*a,  r1 = m_j * bsum32_j
+// Summed over a block's chunks these are the block integers of the CPU
+// vec_dot (k_quants.rs:316-343, 419-440, 513-544, 899-948, 1071-1152, 1524-1605).
+template <int DT>
+__device__ __forceinline__ void chunk_ints(const Chunk& ch, uint32_t c, const int* a, int32_t sv, int& r0, int& r1) {
+    const int bs0 = (int)(int16_t)(sv & 0xffff), bs1 = (int)(int16_t)(sv >> 16);
+    r1 = 0;
+    if (DT == XNQ_Q4_1) {
+        int lo, hi;
+        nib_dot2(ch.q, a, lo, hi);
+        r0 = lo + hi;
+    } else if (DT == XNQ_Q5_0 || DT == XNQ_Q5_1) {
+        const uint32_t q4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
+        int sumi = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t lo = (q4[w] & 0x0F0F0F0Fu) | (spread4(ch.x.y, w) << 4);
+            const uint32_t hi = ((q4[w] >> 4) & 0x0F0F0F0Fu) | (spread4(ch.x.y >> 16, w) << 4);
+            sumi = dot4((int)lo, a[w], sumi);
+            sumi = dot4((int)hi, a[4 + w], sumi);
+        }
+        r0 = DT == XNQ_Q5_0 ? sumi - 16 * sv : sumi;
+    } else if (DT == XNQ_Q2K) {
+        const uint32_t sh = 2 * (c & 3);
+        int i0 = 0, i1 = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            i0 = dot4((int)((dw_of(ch.q, ch.e0, w) >> sh) & 0x03030303u), a[w], i0);
+            i1 = dot4((int)((dw_of(ch.q, ch.e0, w + 4) >> sh) & 0x03030303u), a[4 + w], i1);
+        }
+        const uint32_t scw = (ch.x.y >> (16 * (c & 1))) & 0xffffu;
+        const int s0 = (int)(scw & 0xff), s1 = (int)(scw >> 8);
+        r0 = (s0 & 15) * i0 + (s1 & 15) * i1;
+        r1 = bs0 * (s0 >> 4) + bs1 * (s1 >> 4);
+    } else if (DT == XNQ_Q3K) {
+        // (q3 & 3) - (hmask bit ? 0 : 4), 16-element groups of scale sc - 32
+        const uint32_t sh = 2 * (c & 3), hb = 4 * ((c & 7) >> 2) + (c & 3);
+        int u0 = 0, u1 = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t l0 = ((dw_of(ch.q, ch.e0, w) >> sh) & 0x03030303u) |
+                                (((dw_of(ch.e1, ch.e2, w) >> hb) & 0x01010101u) << 2);
+            const uint32_t l1 = ((dw_of(ch.q, ch.e0, w + 4) >> sh) & 0x03030303u) |
+                                (((dw_of(ch.e1, ch.e2, w + 4) >> hb) & 0x01010101u) << 2);
+            u0 = dot4((int)l0, a[w], u0);
+            u1 = dot4((int)l1, a[4 + w], u1);
+        }
+        const int g = 2 * (int)(c & 7);
+        const int sc0 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g) - 32;
+        const int sc1 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g + 1) - 32;
+        r0 = sc0 * (u0 - 4 * bs0) + sc1 * (u1 - 4 * bs1);
+    } else {  // Q5K
+        const uint32_t j = c & 7, s = j & 1, hb = 2 * (j >> 1) + s;
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t nib = (dw_of(ch.q, ch.e0, w) >> (4 * s)) & 0x0F0F0F0Fu;
+            const uint32_t h5 = ((dw_of(ch.e1, ch.e2, w) >> hb) & 0x01010101u) << 4;
+            v = dot4((int)(nib | h5), a[w], v);
+        }
+        int sc, mn;
+        q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)j, sc, mn);
+        r0 = sc * v;
+        r1 = mn * (bs0 + bs1);
+    }
+}
+
+// f32 combine of one weight chunk c against one activation chunk (a, sv as
+// for chunk_ints), da the activation block scale.  Integer parts are exact; the f32
 // combine follows each type's vec_dot per block.
 template <int DT>
 __device__ __forceinline__ void chunk_fma(const Chunk& ch, uint32_t c, const int* a, int32_t sv, float da,
@@ -264,23 +336,8 @@ __device__ __forceinline__ void chunk_fma(const Chunk& ch, uint32_t c, const int
         acc += (ch.dw * da) * (float)i8_dot32(ch.q, ch.x, a);
     } else if (DT == XNQ_Q4_1 || DT == XNQ_Q5_0 || DT == XNQ_Q5_1) {
         // k_quants.rs:316-343, 419-440, 513-544
-        int sumi;
-        if (DT == XNQ_Q4_1) {
-            int lo, hi;
-            nib_dot2(ch.q, a, lo, hi);
-            sumi = lo + hi;
-        } else {
-            const uint32_t q4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
-            sumi = 0;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const uint32_t lo = (q4[w] & 0x0F0F0F0Fu) | (spread4(ch.x.y, w) << 4);
-                const uint32_t hi = ((q4[w] >> 4) & 0x0F0F0F0Fu) | (spread4(ch.x.y >> 16, w) << 4);
-                sumi = dot4((int)lo, a[w], sumi);
-                sumi = dot4((int)hi, a[4 + w], sumi);
-            }
-            if (DT == XNQ_Q5_0) sumi -= 16 * sv;
-        }
+        int sumi, unused;
+        chunk_ints<DT>(ch, c, a, sv, sumi, unused);
         const float dw = f16_bits_to_f32(ch.x.x);
         float r = (float)sumi * dw * da;
         if (DT != XNQ_Q5_0) {
@@ -292,50 +349,20 @@ __device__ __forceinline__ void chunk_fma(const Chunk& ch, uint32_t c, const int
         acc += r;
     } else if (DT == XNQ_Q2K) {
         // k_quants.rs:899-948: dall * sum_g (sc_g & 15) isum_g - dmin * sum_g (sc_g >> 4) bsum_g
-        const uint32_t sh = 2 * (c & 3);
-        int i0 = 0, i1 = 0;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            i0 = dot4((int)((dw_of(ch.q, ch.e0, w) >> sh) & 0x03030303u), a[w], i0);
-            i1 = dot4((int)((dw_of(ch.q, ch.e0, w + 4) >> sh) & 0x03030303u), a[4 + w], i1);
-        }
-        const uint32_t scw = (ch.x.y >> (16 * (c & 1))) & 0xffffu;
-        const int s0 = (int)(scw & 0xff), s1 = (int)(scw >> 8);
-        const int isum = (s0 & 15) * i0 + (s1 & 15) * i1;
-        const int summs = bs0 * (s0 >> 4) + bs1 * (s1 >> 4);
+        int isum, summs;
+        chunk_ints<DT>(ch, c, a, sv, isum, summs);
         const float dall = da * f16_bits_to_f32(ch.x.x), dmin = da * f16_bits_to_f32(ch.x.x >> 16);
         acc += dall * (float)isum - dmin * (float)summs;
     } else if (DT == XNQ_Q3K) {
-        // k_quants.rs:1071-1152: (q3 & 3) - (hmask bit ? 0 : 4), 16-element groups of scale sc - 32
-        const uint32_t sh = 2 * (c & 3), hb = 4 * ((c & 7) >> 2) + (c & 3);
-        int u0 = 0, u1 = 0;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const uint32_t l0 = ((dw_of(ch.q, ch.e0, w) >> sh) & 0x03030303u) |
-                                (((dw_of(ch.e1, ch.e2, w) >> hb) & 0x01010101u) << 2);
-            const uint32_t l1 = ((dw_of(ch.q, ch.e0, w + 4) >> sh) & 0x03030303u) |
-                                (((dw_of(ch.e1, ch.e2, w + 4) >> hb) & 0x01010101u) << 2);
-            u0 = dot4((int)l0, a[w], u0);
-            u1 = dot4((int)l1, a[4 + w], u1);
-        }
-        const int g = 2 * (int)(c & 7);
-        const int sc0 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g) - 32;
-        const int sc1 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g + 1) - 32;
-        const int isum = sc0 * (u0 - 4 * bs0) + sc1 * (u1 - 4 * bs1);
+        // k_quants.rs:1071-1152
+        int isum, unused;
+        chunk_ints<DT>(ch, c, a, sv, isum, unused);
         acc += (f16_bits_to_f32(ch.x.w) * da) * (float)isum;
     } else {  // Q5K, k_quants.rs:1524-1605
-        const uint32_t j = c & 7, s = j & 1, hb = 2 * (j >> 1) + s;
-        int v = 0;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            const uint32_t nib = (dw_of(ch.q, ch.e0, w) >> (4 * s)) & 0x0F0F0F0Fu;
-            const uint32_t h5 = ((dw_of(ch.e1, ch.e2, w) >> hb) & 0x01010101u) << 4;
-            v = dot4((int)(nib | h5), a[w], v);
-        }
-        int sc, mn;
-        q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)j, sc, mn);
+        int isum, msum;
+        chunk_ints<DT>(ch, c, a, sv, isum, msum);
         const float d = f16_bits_to_f32(ch.x.x) * da, dmin = f16_bits_to_f32(ch.x.x >> 16) * da;
-        acc += d * (float)(sc * v) - dmin * (float)(mn * (bs0 + bs1));
+        acc += d * (float)isum - dmin * (float)msum;
     }
 }
 

@@ -721,8 +721,6 @@ xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* w
     if (!qt) return fail(XNQ_ERR_INVALID, "null qtensor");
     if (m == 0) return XNQ_OK;
     if (!workspace_dev || !out_dev) return fail(XNQ_ERR_INVALID, "null pointer");
-    if (is_raw_layout(qt->L.dtype))
-        return fail(XNQ_ERR_UNSUPPORTED, "block_ints covers Q4_0, Q8_0, Q4K and Q6K");
     DeviceGuard g(qt->device);
     const WView w = make_wview(qt->L, qt->buf);
     const AView a = make_aview(act_layout(qt->L.dtype, m, qt->L.k), workspace_dev);
