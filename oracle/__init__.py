@@ -143,7 +143,8 @@ def matmul_preq(dt: int, lhs_blocks: np.ndarray, w_blocks: np.ndarray, m: int, k
 
 def block_ints(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: int, k: int) -> np.ndarray:
     """int64 [m, n, nb, 2]: the integer parts of every block dot, as the CPU
-    vec_dot forms them (see orc_q4k_block_ints / orc_q6k_block_ints)."""
+    vec_dot forms them (the K types through orc_q*k_block_ints; the 32-element
+    types as their block integer sums, restated here)."""
     bs = BLOCK_SIZE[dt]
     nb = k // bs
     vt = vec_dot_type(dt)
@@ -164,6 +165,24 @@ def block_ints(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: i
                     tmp[:] = 0
                     fn(wb.ctypes.data, ab.ctypes.data, tmp.ctypes.data)
                     out[r, c, b] = tmp
+        return out
+    if dt in (Q4_1, Q5_0, Q5_1):
+        # k_quants.rs:316-343 / 419-440 / 513-544: sum_i q_i * a_i per 32-block,
+        # q from the nibble (and Q5's fifth bit qh >> i), Q5_0 offset by -16
+        vb = TYPE_SIZE[vt]  # Q8_1 (36 B: d, s, qs) or Q8_0 (34 B: d, qs)
+        aq = a_blocks.reshape(m, nb, vb)[:, :, vb - 32:].view(np.int8).astype(np.int64)
+        ts = TYPE_SIZE[dt]
+        qs_off = {Q4_1: 4, Q5_0: 6, Q5_1: 8}[dt]
+        qs = wv[:, :, qs_off:qs_off + 16].astype(np.int64)
+        wq = np.concatenate([qs & 0xF, qs >> 4], axis=2)
+        if dt != Q4_1:
+            qh_off = 2 if dt == Q5_0 else 4
+            qh = wv[:, :, qh_off:qh_off + 4].copy().view(np.uint32)[:, :, 0].astype(np.int64)
+            wq = wq | (((qh[:, :, None] >> np.arange(32)[None, None, :]) & 1) << 4)
+            if dt == Q5_0:
+                wq = wq - 16
+        assert ts == wv.shape[2]
+        out[..., 0] = np.einsum("mbe,nbe->mnb", aq, wq)
         return out
     # Q4_0 / Q8_0: integer block sums, vectorised
     av = a_blocks.reshape(m, nb, 34)

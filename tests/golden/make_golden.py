@@ -26,6 +26,12 @@ CASES = [
     ("q4_0", oracle.Q4_0, 3, 256, 16),
     ("q4k", oracle.Q4K, 3, 512, 16),
     ("q6k", oracle.Q6K, 3, 512, 16),
+    ("q4_1", oracle.Q4_1, 3, 256, 16),
+    ("q5_0", oracle.Q5_0, 3, 256, 16),
+    ("q5_1", oracle.Q5_1, 3, 256, 16),
+    ("q2k", oracle.Q2K, 3, 512, 16),
+    ("q3k", oracle.Q3K, 3, 512, 16),
+    ("q5k", oracle.Q5K, 3, 512, 16),
 ]
 SEED = 299792458
 

@@ -22,7 +22,7 @@ def load(path):
 
 
 def test_fixtures_present():
-    assert len(FIXTURES) == 4
+    assert len(FIXTURES) == 10
 
 
 @pytest.mark.parametrize("path", FIXTURES, ids=IDS)
@@ -51,13 +51,25 @@ def test_device_matches_golden(dev, path):
     dt, m, k, n = int(g["dtype"]), int(g["m"]), int(g["k"]), int(g["n"])
     w = torch.from_numpy(g["w"]).to(dev)
     x = torch.from_numpy(g["x"]).to(dev)
-    # device weight quantizer
-    qt = QTensor.quantize_f32(w, (n, k), GgmlDType(dt))
-    assert qt.data() == g["w_blocks"].tobytes()
+    if dt in (GgmlDType.Q4_0, GgmlDType.Q8_0, GgmlDType.Q4K, GgmlDType.Q6K):
+        # device weight quantizer
+        qt = QTensor.quantize_f32(w, (n, k), GgmlDType(dt))
+        assert qt.data() == g["w_blocks"].tobytes()
+    else:
+        # no device quantizer for this dtype (xn quantizes on the host): upload
+        qt = QTensor.from_gguf_bytes(g["w_blocks"], (n, k), GgmlDType(dt), dev)
+        assert qt.data() == g["w_blocks"].tobytes()
     # device activation quantizer, canonical blocks
-    act = GgmlDType.Q8_0 if dt in (GgmlDType.Q4_0, GgmlDType.Q8_0) else GgmlDType.Q8K
+    kq = dt in (GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
+    act = GgmlDType.Q8K if kq else GgmlDType.Q8_0
     got_ab = quantize_act_blocks(act, x, m, k).cpu().numpy()
-    assert np.array_equal(got_ab.reshape(-1), g["act_blocks"].reshape(-1))
+    if dt in (GgmlDType.Q4_1, GgmlDType.Q5_1):
+        # Q8_1 blocks (d, s, qs): the device's Q8_0 blocks carry the same d and qs
+        want = g["act_blocks"].reshape(-1, 36)
+        got = got_ab.reshape(-1, 34)
+        assert np.array_equal(got[:, :2], want[:, :2]) and np.array_equal(got[:, 2:], want[:, 4:])
+    else:
+        assert np.array_equal(got_ab.reshape(-1), g["act_blocks"].reshape(-1))
     # integer block dots
     ws = lhs_workspace(qt.dtype(), m, k, dev)
     quantize_lhs(qt.dtype(), x, ws, m, k)

@@ -168,7 +168,7 @@ def test_make_q3_quants_degenerate_and_grid(orc):
     assert np.allclose((ls.astype(np.float32) - 4) * s, x, atol=1e-6)
 
 
-@pytest.mark.parametrize("dt", [Q2K, Q3K, Q5K])
+@pytest.mark.parametrize("dt", [Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K])
 def test_kquant_block_ints_bruteforce(orc, dt):
     rng = np.random.default_rng(140 + dt)
     m, n, k = 3, 5, 512
