@@ -525,7 +525,11 @@ __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* _
     const uint32_t k = G.w[0].k;
     const ActImg A = act_img(k, kq);
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = threadIdx.x / kWave;
+    // wavefront-uniform in an SGPR: the weight view G.w[t] of a row is then
+    // read with scalar loads; indexed by a VGPR it is read with vector loads,
+    // whose in-order wait would also wait for the activation load issued
+    // before them and hold back the whole weight stream
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t nchunks = k / 32;
     const uint32_t npass = (nchunks + 64 * CPL - 1) / (64 * CPL);
     const uint32_t row0 = (blockIdx.x * NW + wave) * R;
@@ -566,6 +570,8 @@ __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* _
     XQuant<DT, 1, NW, (CPL * 64 + NW * 128 - 1) / (NW * 128)> xq;  // one round covers K = 64 * CPL * 32
     xq.load(x, k, 0, 1, xq.first(wave), lane);
     issue(0);
+    // every weight load is issued before the quantizer's first use of x
+    __builtin_amdgcn_sched_barrier(0);
     xq.quant(lds, A, k, xq.first(wave), lane);
     xq.rest(x, k, 0, 1, lds, A, wave, lane);
     __syncthreads();

@@ -50,18 +50,34 @@ namespace xnq {
 namespace {
 
 // y = sum of the split-K partial outputs, in split order (deterministic).
+// The loads of up to 8 splits are issued together (addresses clamped to the
+// last split, values past it never added), so a call costs one memory round
+// trip per 8 splits rather than one per split.
 __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part, size_t count,
                                                          uint32_t splits, float* __restrict__ y) {
+    constexpr uint32_t kBatch = 8;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (count % 4 == 0) {
         if (i4 * 4 >= count) return;
-        float4 acc = reinterpret_cast<const float4*>(part)[i4];
-        for (uint32_t z = 1; z < splits; z++) {
-            const float4 v = reinterpret_cast<const float4*>(part + z * count)[i4];
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
+        const float4* p4 = reinterpret_cast<const float4*>(part);
+        const size_t c4 = count / 4;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t z0 = 0; z0 < splits; z0 += kBatch) {
+            float4 v[kBatch];
+#pragma unroll
+            for (uint32_t j = 0; j < kBatch; j++) v[j] = p4[min(z0 + j, splits - 1) * c4 + i4];
+#pragma unroll
+            for (uint32_t j = 0; j < kBatch; j++) {
+                if (z0 + j >= splits) break;
+                if (z0 + j == 0) {
+                    acc = v[0];
+                } else {
+                    acc.x += v[j].x;
+                    acc.y += v[j].y;
+                    acc.z += v[j].z;
+                    acc.w += v[j].w;
+                }
+            }
         }
         reinterpret_cast<float4*>(y)[i4] = acc;
         return;
