@@ -477,21 +477,33 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
 
 // Decode: the fused matvec route quantizes the activation row in LDS inside
 // the matvec kernel and needs no workspace.  It saves the quantize launch
-// (~1.8 us) but streams the weights more slowly than the plain matvec kernel,
-// by an amount that grows with the weight (measured at m = 1: +0.7 us at
-// 4096 x 4096, +4.7 us at 4096 -> 14336, +17 us at 8192 -> 28672) and with m
-// (m = 2, 14336 -> 4096: 23 us against 11 + 1.8), so it takes m = 1 on
-// weights of up to XNQ_FUSED_MAX_ELEMS (6144 x 4096) elements only.
+// (~1.8 us), but every workgroup quantizes the whole row, so on large
+// weights it streams more slowly than quantize + matvec (measured at m = 1:
+// 4096 -> 14336: 9.6 against 9.45 us; 14336 -> 4096 Q6_K: 14.2 against 13.2;
+// 8192 -> 28672: 36.9 against 25.0) and with m (m = 2, 14336 -> 4096: 23 us
+// against 11 + 1.8).  A single matmul_t takes it for m = 1 on weights of up
+// to XNQ_FUSED_MAX_ELEMS (6144 x 4096) elements.  The q/k/v group and the
+// SiLU-gated gate/up pair take it whenever K <= XNQ_FUSED_MAX_K (4096): one
+// launch for several weights wins there (decode step 1540 -> 1432 us).
 static size_t fused_max_elems() {
     static const size_t v = env_size("XNQ_FUSED_MAX_ELEMS", (size_t)6144 * 4096);
     return v;
 }
 
-static bool fused_route(const xnq_qtensor* qt, size_t m) {
+// Rows of at most this K take the fused m = 1 kernel at any N.
+static size_t fused_max_k() {
+    static const size_t v = env_size("XNQ_FUSED_MAX_K", 4096);
+    return v;
+}
+
+// `grouped`: the weight is one of a q/k/v group or a gate/up pair, whose
+// one-launch kernels take K <= XNQ_FUSED_MAX_K at any N; a single matmul_t
+// takes the element limit alone.
+static bool fused_route(const xnq_qtensor* qt, size_t m, bool grouped = false) {
     const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k);
     if (r != kMatvec) return false;
     if (g_route.load() == 1) return true;
-    return m == 1 && qt->L.n * qt->L.k <= fused_max_elems();
+    return m == 1 && ((grouped && qt->L.k <= fused_max_k()) || qt->L.n * qt->L.k <= fused_max_elems());
 }
 
 size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m) {
@@ -558,7 +570,7 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
 static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m) {
     if (m != 1 || count == 0 || count > (size_t)kMaxGroup) return false;
     for (size_t i = 0; i < count; i++) {
-        if (!qts[i] || !fused_route(qts[i], m)) return false;
+        if (!qts[i] || !fused_route(qts[i], m, true)) return false;
         if (qts[i]->L.dtype != qts[0]->L.dtype || qts[i]->L.k != qts[0]->L.k || qts[i]->device != qts[0]->device)
             return false;
     }
