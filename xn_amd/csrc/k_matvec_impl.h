@@ -274,7 +274,7 @@ __device__ __forceinline__ void chunk_ints(const Chunk& ch, uint32_t c, const in
         }
         const uint32_t scw = (ch.x.y >> (16 * (c & 1))) & 0xffffu;
         const int s0 = (int)(scw & 0xff), s1 = (int)(scw >> 8);
-        r0 = (s0 & 15) * i0 + (s1 & 15) * i1;
+        r0 = __mul24(s0 & 15, i0) + __mul24(s1 & 15, i1);  // |i| <= 16*3*128
         r1 = bs0 * (s0 >> 4) + bs1 * (s1 >> 4);
     } else if (DT == XNQ_Q3K) {
         // (q3 & 3) - (hmask bit ? 0 : 4), 16-element groups of scale sc - 32
@@ -292,7 +292,7 @@ __device__ __forceinline__ void chunk_ints(const Chunk& ch, uint32_t c, const in
         const int g = 2 * (int)(c & 7);
         const int sc0 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g) - 32;
         const int sc1 = (int)(int8_t)q3k_scale(ch.x.x, ch.x.y, ch.x.z, g + 1) - 32;
-        r0 = sc0 * (u0 - 4 * bs0) + sc1 * (u1 - 4 * bs1);
+        r0 = __mul24(sc0, u0 - 4 * bs0) + __mul24(sc1, u1 - 4 * bs1);  // |u - 4 bs| < 2^16
     } else {  // Q5K
         const uint32_t j = c & 7, s = j & 1, hb = 2 * (j >> 1) + s;
         int v = 0;
@@ -304,7 +304,7 @@ __device__ __forceinline__ void chunk_ints(const Chunk& ch, uint32_t c, const in
         }
         int sc, mn;
         q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)j, sc, mn);
-        r0 = sc * v;
+        r0 = __mul24(sc, v);  // |v| <= 32*31*128 < 2^23
         r1 = mn * (bs0 + bs1);
     }
 }
@@ -321,9 +321,10 @@ __device__ __forceinline__ void chunk_fma(const Chunk& ch, uint32_t c, const int
         const float dw = f16_bits_to_f32(ch.x.x), dmin = f16_bits_to_f32(ch.x.x >> 16);
         q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)(c & 7), sc, mn);
         nib_dot2(ch.q, a, lo, hi);
-        const int isum = sc * (lo + hi);
-        const int msum = mn * (bs0 + bs1);
-        acc += (dw * da) * (float)isum - (dmin * da) * (float)msum;
+        // |lo + hi| <= 32*15*128 < 2^23: the 24-bit multiply is exact
+        const int isum = __mul24(sc, lo + hi);
+        const int msum = __mul24(mn, bs0 + bs1);
+        acc = fmaf(da, fmaf(dw, (float)isum, -(dmin * (float)msum)), acc);
     } else if (DT == XNQ_Q6K) {
         const int sc0 = (int)(int8_t)(ch.x.z & 0xff), sc1 = (int)(int8_t)((ch.x.z >> 8) & 0xff);
         const int v = q6k_chunk_int(ch.q, make_uint2(ch.x.x, ch.x.y), a, sc0, sc1, bs0, bs1);

@@ -577,6 +577,19 @@ static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m) {
     return true;
 }
 
+// Off the one-launch route, weights of one dtype, K and device that all
+// take a quantized workspace share one quantize launch: the activation image
+// depends only on the dtype, m and K.
+static bool shared_quantize(const xnq_qtensor* const* qts, size_t count, size_t m) {
+    if (count < 2) return false;
+    for (size_t i = 0; i < count; i++) {
+        if (!qts[i] || fused_route(qts[i], m)) return false;
+        if (qts[i]->L.dtype != qts[0]->L.dtype || qts[i]->L.k != qts[0]->L.k || qts[i]->device != qts[0]->device)
+            return false;
+    }
+    return true;
+}
+
 static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* const* dsts) {
     WGroup g{};
     uint32_t end = 0;
@@ -630,8 +643,17 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     const size_t a = xnq_qtensor_matmul_t_workspace_size(gate, m), b = xnq_qtensor_matmul_t_workspace_size(up, m);
     const size_t off = align_up(a > b ? a : b, kAlign);
     float* u = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + off);
-    st = xnq_qtensor_matmul_t_ws(gate, m, k, n, lhs_dev, workspace_dev, off, dst_dev, stream);
-    if (!st) st = xnq_qtensor_matmul_t_ws(up, m, k, n, lhs_dev, workspace_dev, off, u, stream);
+    const xnq_qtensor* pair[2] = {gate, up};
+    if (shared_quantize(pair, 2, m)) {
+        DeviceGuard g(gate->device);
+        if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+        st = xnq_quantize_lhs(gate->L.dtype, m, k, lhs_dev, workspace_dev, stream);
+        if (!st) st = xnq_qtensor_matmul_preq(gate, m, k, n, workspace_dev, off, dst_dev, stream);
+        if (!st) st = xnq_qtensor_matmul_preq(up, m, k, n, workspace_dev, off, u, stream);
+    } else {
+        st = xnq_qtensor_matmul_t_ws(gate, m, k, n, lhs_dev, workspace_dev, off, dst_dev, stream);
+        if (!st) st = xnq_qtensor_matmul_t_ws(up, m, k, n, lhs_dev, workspace_dev, off, u, stream);
+    }
     if (st) return st;
     DeviceGuard g(gate->device);
     const hipError_t e = launch_silu_mul(dst_dev, u, m * n, s);
@@ -670,6 +692,20 @@ xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_
         const hipError_t e = launch_matvec_group(make_group(qts, count, dsts_dev), lhs_dev, false, (hipStream_t)stream);
         if (e != hipSuccess) return hip_fail(e, "grouped matvec kernel");
         return XNQ_OK;
+    }
+    if (shared_quantize(qts, count, m)) {
+        // one activation image for every weight, then one matmul each
+        const size_t need = act_layout(qts[0]->L.dtype, m, k).bytes;
+        if (!workspace_dev || workspace_bytes < need)
+            return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu the activation needs",
+                        workspace_bytes, need);
+        DeviceGuard g(qts[0]->device);
+        if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+        xnq_status st = xnq_quantize_lhs(qts[0]->L.dtype, m, k, lhs_dev, workspace_dev, stream);
+        for (size_t i = 0; i < count && !st; i++)
+            st = xnq_qtensor_matmul_preq(qts[i], m, k, qts[i]->L.n, workspace_dev, workspace_bytes, dsts_dev[i],
+                                         stream);
+        return st;
     }
     for (size_t i = 0; i < count; i++) {
         const xnq_status st = xnq_qtensor_matmul_t_ws(qts[i], m, k, qts[i]->L.n, lhs_dev, workspace_dev,

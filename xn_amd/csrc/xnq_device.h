@@ -134,7 +134,8 @@ __device__ __forceinline__ int q6k_chunk_int(uint4 ql, uint2 qh, const int* a, i
     hi = dot4(b[5], a[5], hi);
     hi = dot4(b[6], a[6], hi);
     hi = dot4(b[7], a[7], hi);
-    return sc0 * (lo - 32 * bs0) + sc1 * (hi - 32 * bs1);
+    // |lo - 32*bs0| <= 16*63*128 + 32*16*128 < 2^23: the 24-bit multiply is exact
+    return __mul24(sc0, lo - 32 * bs0) + __mul24(sc1, hi - 32 * bs1);
 }
 
 // Sum of 32 signed bytes x signed bytes.
