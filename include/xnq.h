@@ -128,15 +128,19 @@ xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, si
  * llama.rs:258-264 (Mlp::forward) with silu(s) = s / (1 + exp(0 - s))
  * (cpu_backend.rs:354-356); gate and up have one shape.  m == 1 with both on
  * the one-launch route (K <= 4096 at any N, or weights of up to 6144 x 4096
- * elements) and K <= 10240 is one kernel and needs no workspace; otherwise
- * one activation quantize serves both products (matmul_preq each), then a
- * SiLU-multiply kernel, with workspace for the second product.
+ * elements) and K <= 10240 is one kernel and needs no workspace; on the
+ * small-batch MFMA route (Q4_K/Q6_K, 12 <= m <= 64) one quantize, one
+ * launch over both weights and one split-sum that applies the SiLU-multiply;
+ * otherwise one activation quantize serves both products (matmul_preq
+ * each), then a SiLU-multiply kernel, with workspace for the second product.
  *
  * group: dsts[i][m x n_i] = lhs . qts[i]^T for up to 3 weights of one dtype
  * and K (the q, k, v projections of llama.rs:156-158); m == 1 on the
- * one-launch route is one kernel over the joined rows; otherwise weights of
- * one dtype and K share one activation quantize (matmul_preq each), and other
- * groups take one matmul_t_ws per weight.  Workspace sizes are 0 when the
+ * one-launch route is one kernel over the joined rows; on the small-batch
+ * MFMA route one quantize, one launch over the joined column tiles and one
+ * split-sum; otherwise weights of one dtype and K share one activation
+ * quantize (matmul_preq each), and other groups take one matmul_t_ws per
+ * weight.  Workspace sizes are 0 when the
  * single-kernel route applies. */
 size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m);
 xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,

@@ -89,7 +89,51 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict
     }
 }
 
+// Sum of `splits` consecutive partials of one element, in split order, the
+// loads of up to 8 splits issued together.
+__device__ __forceinline__ float sum_over_splits(const float* __restrict__ p, size_t stride, uint32_t splits) {
+    constexpr uint32_t kBatch = 8;
+    float acc = 0.0f;
+    for (uint32_t z0 = 0; z0 < splits; z0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; j++) v[j] = p[min(z0 + j, splits - 1) * stride];
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; j++) {
+            if (z0 + j >= splits) break;
+            acc = z0 + j == 0 ? v[0] : acc + v[j];
+        }
+    }
+    return acc;
+}
+
+// Element i of the regions laid end to end; silu: y[0] = silu(g) * u over
+// region 0's elements (cpu_backend.rs:354-356).
+__global__ __launch_bounds__(256) void sum_group_kernel(SumGroup S, uint32_t splits, bool silu) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (silu) {
+        if (i >= S.cnt[0]) return;
+        const float g = sum_over_splits(S.part[0] + i, S.cnt[0], splits);
+        const float u = sum_over_splits(S.part[1] + i, S.cnt[1], splits);
+        S.y[0][i] = g / (1.0f + expf(0.0f - g)) * u;
+        return;
+    }
+    uint32_t t = 0;
+    while (t < S.count && i >= S.cnt[t]) i -= S.cnt[t++];
+    if (t >= S.count) return;
+    S.y[t][i] = sum_over_splits(S.part[t] + i, S.cnt[t], splits);
+}
+
 }  // namespace
+
+hipError_t launch_sum_group(const SumGroup& S, uint32_t splits, bool silu, hipStream_t s) {
+    size_t total = 0;
+    for (uint32_t t = 0; t < S.count; t++) total += S.cnt[t];
+    if (silu) total = S.cnt[0];
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(sum_group_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, S, splits, silu);
+    return hipGetLastError();
+}
 
 hipError_t launch_sum_splits(const float* partial, size_t count, uint32_t splits, float* y, hipStream_t s) {
     const unsigned blocks = (unsigned)((count / 4 + 255) / 256 + 1);

@@ -128,9 +128,21 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
     return make_uint4(hu.x, hu.y, lu.x, lu.y);
 }
 
+// Where each weight of a launch writes: y[t] (the destination, or its
+// split-K partial region of `stride[t]` floats per split) for the column
+// tiles below tile_end[t] (cumulative over the group).
+struct SkOut {
+    float* y[kMaxGroup];
+    size_t stride[kMaxGroup];
+    uint32_t tile_end[kMaxGroup];
+};
+
+// One launch covers the column tiles of up to kMaxGroup weights of one dtype
+// and K (G.w[0..count)): a workgroup's tile picks its weight, uniformly, so
+// the weight view is read with scalar loads.
 template <int DT, int MT, int NW>
-__global__ __launch_bounds__(64 * NW) void skinny_kernel(WView w, AView a, uint32_t m, uint32_t sb_per_split,
-                                                          float* __restrict__ y, size_t split_stride) {
+__global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AView a, uint32_t m,
+                                                          uint32_t sb_per_split) {
     using L = KLay<DT, MT, NW>;
     constexpr int kCols = L::kCols;
     constexpr bool kQ4K = L::kQ4K;
@@ -141,10 +153,13 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WView w, AView a, uint3
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lrow = lane & 31, half = lane >> 5;
+    const uint32_t bx = blockIdx.x;
+    const uint32_t t = G.count > 1 && bx >= O.tile_end[0] ? (G.count > 2 && bx >= O.tile_end[1] ? 2u : 1u) : 0u;
+    const WView w = G.w[t];
+    float* __restrict__ y = O.y[t] + blockIdx.y * O.stride[t];
     const uint32_t sb0 = blockIdx.y * sb_per_split;
     const uint32_t nsb = min(sb_per_split, w.k / 256 - sb0);
-    y += blockIdx.y * split_stride;
-    const uint32_t col0 = blockIdx.x * kCols;
+    const uint32_t col0 = (bx - (t > 0 ? O.tile_end[t - 1] : 0u)) * kCols;
     const uint32_t ncol = col0 + wave * 32 + lrow;  // this lane's output column
     const uint32_t lbase = (uint32_t)(uintptr_t)lds;  // low half of the flat address = LDS offset
     const ActImg& A = a.A;
@@ -341,7 +356,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WView w, AView a, uint3
 }
 
 template <int DT, int MT, int NW>
-hipError_t launch_skinny_dt(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
+hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
                             hipStream_t s) {
     using L = KLay<DT, MT, NW>;
     constexpr int kCols = L::kCols;
@@ -352,16 +367,32 @@ hipError_t launch_skinny_dt(const WView& w, const AView& a, size_t m, uint32_t s
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const uint32_t nsb = w.k / 256;
+    const uint32_t nsb = G.w[0].k / 256;
     const uint32_t per = (nsb + splits - 1) / splits;
     splits = (nsb + per - 1) / per;  // every split non-empty
-    const dim3 grid((w.n + kCols - 1) / kCols, splits);
-    float* out = splits > 1 ? partial : y;
-    hipLaunchKernelGGL((skinny_kernel<DT, MT, NW>), grid, dim3(L::kThreads), L::kLds, s, w, a, (uint32_t)m, per, out,
-                       splits > 1 ? m * (size_t)w.n : (size_t)0);
+    // partial regions, weight after weight: [split][m][n_t]
+    const bool reduce = splits > 1 || silu;
+    SkOut O{};
+    SumGroup S{};
+    uint32_t tiles = 0;
+    size_t off = 0;
+    for (uint32_t t = 0; t < G.count; t++) {
+        const size_t cnt = m * (size_t)G.w[t].n;
+        tiles += (G.w[t].n + kCols - 1) / kCols;
+        O.tile_end[t] = tiles;
+        O.y[t] = reduce ? partial + off : G.y[t];
+        O.stride[t] = reduce ? cnt : 0;
+        S.part[t] = partial + off;
+        S.y[t] = G.y[t];
+        S.cnt[t] = cnt;
+        off += splits * cnt;
+    }
+    S.count = G.count;
+    const dim3 grid(tiles, splits);
+    hipLaunchKernelGGL((skinny_kernel<DT, MT, NW>), grid, dim3(L::kThreads), L::kLds, s, G, O, a, (uint32_t)m, per);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || splits == 1) return e;
-    return launch_sum_splits(partial, m * (size_t)w.n, splits, y, s);
+    if (e != hipSuccess || !reduce) return e;
+    return launch_sum_group(S, splits, silu, s);
 }
 
 }  // namespace
@@ -397,24 +428,39 @@ bool skinny_supported(uint32_t dtype, size_t m, size_t n, size_t k) {
     return (dtype == XNQ_Q4K || dtype == XNQ_Q6K) && k % 256 == 0 && m >= 1 && m <= 64;
 }
 
-hipError_t launch_skinny(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
-                         hipStream_t s) {
-    if (m == 0 || w.n == 0) return hipSuccess;
-    if (m > 64) return hipErrorInvalidValue;
+hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
+                               hipStream_t s) {
+    if (m == 0 || G.count == 0) return hipSuccess;
+    if (m > 64 || G.count > (uint32_t)kMaxGroup || (silu && G.count != 2)) return hipErrorInvalidValue;
+    if (silu && !partial) return hipErrorInvalidValue;
     if (splits > 1 && !partial) splits = 1;
-    const bool w8 = skinny_waves(w.n, w.k) == 8;
+    size_t n = 0;
+    for (uint32_t t = 0; t < G.count; t++) n += G.w[t].n;
+    const bool w8 = skinny_waves(n, G.w[0].k) == 8;
 #define XNQ_SK(DT)                                                                                   \
-    if (w.dtype == DT) {                                                                             \
+    if (G.w[0].dtype == DT) {                                                                        \
         if (m <= 32)                                                                                 \
-            return w8 ? launch_skinny_dt<DT, 1, 8>(w, a, m, splits, y, partial, s)                  \
-                      : launch_skinny_dt<DT, 1, 4>(w, a, m, splits, y, partial, s);                 \
-        return w8 ? launch_skinny_dt<DT, 2, 8>(w, a, m, splits, y, partial, s)                      \
-                  : launch_skinny_dt<DT, 2, 4>(w, a, m, splits, y, partial, s);                     \
+            return w8 ? launch_skinny_dt<DT, 1, 8>(G, a, m, splits, partial, silu, s)               \
+                      : launch_skinny_dt<DT, 1, 4>(G, a, m, splits, partial, silu, s);              \
+        return w8 ? launch_skinny_dt<DT, 2, 8>(G, a, m, splits, partial, silu, s)                   \
+                  : launch_skinny_dt<DT, 2, 4>(G, a, m, splits, partial, silu, s);                  \
     }
     XNQ_SK(XNQ_Q4K)
     XNQ_SK(XNQ_Q6K)
 #undef XNQ_SK
     return hipErrorNotSupported;
+}
+
+hipError_t launch_skinny(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
+                         hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    WGroup G{};
+    G.w[0] = w;
+    G.y[0] = y;
+    G.row_end[0] = w.n;
+    G.count = 1;
+    G.rows = w.n;
+    return launch_skinny_group(G, a, m, splits, partial, false, s);
 }
 
 }  // namespace xnq

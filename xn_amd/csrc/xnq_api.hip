@@ -590,6 +590,35 @@ static bool shared_quantize(const xnq_qtensor* const* qts, size_t count, size_t 
     return true;
 }
 
+// Weights that share one quantize and all take the skinny route run as one
+// skinny launch over their joined column tiles, with one split-K sum.
+static bool skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m) {
+    if (!shared_quantize(qts, count, m)) return false;
+    for (size_t i = 0; i < count; i++) {
+        const WLayout& L = qts[i]->L;
+        if (pick_route(L.dtype, m, L.n, L.k) != kSkinny || !skinny_supported(L.dtype, m, L.n, L.k)) return false;
+    }
+    return true;
+}
+
+static size_t joined_n(const xnq_qtensor* const* qts, size_t count) {
+    size_t n = 0;
+    for (size_t i = 0; i < count; i++) n += qts[i]->L.n;
+    return n;
+}
+
+// Activation image, then one partial region per weight ([split][m][n_t]).
+static size_t skinny_group_ws(const xnq_qtensor* const* qts, size_t count, size_t m) {
+    const size_t k = qts[0]->L.k, n = joined_n(qts, count);
+    return partial_offset(qts[0]->L.dtype, m, k) + (size_t)skinny_splits(m, n, k) * m * n * sizeof(float);
+}
+
+// Quantize once, then the skinny kernel over the group (silu: gate, up pair
+// into G.y[0]).
+static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
+                                   const float* lhs_dev, float* const* dsts, void* workspace_dev,
+                                   size_t workspace_bytes, bool silu, void* stream);
+
 static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* const* dsts) {
     WGroup g{};
     uint32_t end = 0;
@@ -604,12 +633,35 @@ static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* con
     return g;
 }
 
+static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
+                                   const float* lhs_dev, float* const* dsts, void* workspace_dev,
+                                   size_t workspace_bytes, bool silu, void* stream) {
+    const uint32_t dt = qts[0]->L.dtype;
+    const size_t need = skinny_group_ws(qts, count, m);
+    if (!workspace_dev || workspace_bytes < need)
+        return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
+    DeviceGuard g(qts[0]->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    xnq_status st = xnq_quantize_lhs(dt, m, k, lhs_dev, workspace_dev, stream);
+    if (st) return st;
+    const WGroup G = make_group(qts, count, dsts);
+    const AView a = make_aview(act_layout(dt, m, k), workspace_dev);
+    float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + partial_offset(dt, m, k));
+    const hipError_t e = launch_skinny_group(G, a, m, skinny_splits(m, joined_n(qts, count), k), partial, silu,
+                                             (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "grouped skinny kernel");
+    return XNQ_OK;
+}
+
 size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m) {
     if (!gate || !up) return 0;
     const xnq_qtensor* pair[2] = {gate, up};
     if (group_route(pair, 2, m) && gate->L.k <= 64 * 5 * 32) return 0;
     const size_t a = xnq_qtensor_matmul_t_workspace_size(gate, m), b = xnq_qtensor_matmul_t_workspace_size(up, m);
-    return align_up(a > b ? a : b, kAlign) + m * up->L.n * sizeof(float);
+    const size_t two = align_up(a > b ? a : b, kAlign) + m * up->L.n * sizeof(float);
+    if (gate->L.n != up->L.n || !skinny_group(pair, 2, m)) return two;
+    const size_t one = skinny_group_ws(pair, 2, m);
+    return one > two ? one : two;
 }
 
 xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
@@ -644,6 +696,10 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     const size_t off = align_up(a > b ? a : b, kAlign);
     float* u = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + off);
     const xnq_qtensor* pair[2] = {gate, up};
+    if (skinny_group(pair, 2, m)) {
+        float* dsts[2] = {dst_dev, nullptr};
+        return run_skinny_group(pair, 2, m, k, lhs_dev, dsts, workspace_dev, workspace_bytes, true, stream);
+    }
     if (shared_quantize(pair, 2, m)) {
         DeviceGuard g(gate->device);
         if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
@@ -667,6 +723,10 @@ size_t xnq_matmul_t_group_workspace_size(const xnq_qtensor* const* qts, size_t c
     for (size_t i = 0; i < count; i++) {
         const size_t b = qts[i] ? xnq_qtensor_matmul_t_workspace_size(qts[i], m) : 0;
         if (b > need) need = b;
+    }
+    if (count <= (size_t)kMaxGroup && skinny_group(qts, count, m)) {
+        const size_t one = skinny_group_ws(qts, count, m);
+        if (one > need) need = one;
     }
     return need;
 }
@@ -693,6 +753,8 @@ xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_
         if (e != hipSuccess) return hip_fail(e, "grouped matvec kernel");
         return XNQ_OK;
     }
+    if (count <= (size_t)kMaxGroup && skinny_group(qts, count, m))
+        return run_skinny_group(qts, count, m, k, lhs_dev, dsts_dev, workspace_dev, workspace_bytes, false, stream);
     if (shared_quantize(qts, count, m)) {
         // one activation image for every weight, then one matmul each
         const size_t need = act_layout(qts[0]->L.dtype, m, k).bytes;

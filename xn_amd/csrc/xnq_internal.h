@@ -221,6 +221,21 @@ hipError_t launch_skinny(const WView& w, const AView& a, size_t m, uint32_t spli
                          hipStream_t s);
 // y[i] = sum over z < splits of partial[z * count + i], in z order
 hipError_t launch_sum_splits(const float* partial, size_t count, uint32_t splits, float* y, hipStream_t s);
+// Split-K sums of up to kMaxGroup partial regions (region t: [split][cnt[t]]
+// floats at part[t]) into y[t]; `silu` (two regions of one size): y[0] =
+// silu(sum 0) * sum 1 with silu(s) = s / (1 + exp(0 - s)).
+struct SumGroup {
+    const float* part[kMaxGroup];
+    float* y[kMaxGroup];
+    size_t cnt[kMaxGroup];
+    uint32_t count;
+};
+hipError_t launch_sum_group(const SumGroup& S, uint32_t splits, bool silu, hipStream_t s);
+// The skinny kernel over a group of weights of one dtype and K (G.w, G.y,
+// G.count; G.row_end unused) in one launch; `silu` (two weights of one
+// shape) writes silu(x . w0) * (x . w1) to G.y[0] and needs `partial`.
+hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
+                               hipStream_t s);
 hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                        hipStream_t s);
 
