@@ -271,12 +271,18 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
             } else {
                 const uint2 qh = *reinterpret_cast<const uint2*>(S + L::kWh + cl * 64 + (((c >> 1) ^ (cl & 3)) * 16) +
                                                                  (c & 1) * 8);
-                int b[8];
-                q6k_unpack(qc, qh, b);
+                // this lane's 16 elements: low (half 0) or high (half 1)
+                // nibbles of ql, the two high bits from qh word `half`
+                // (the q6k_unpack bit layout, one half of it)
+                const uint32_t qhw = half ? qh.y : qh.x;
+                const uint32_t q4[4] = {qc.x, qc.y, qc.z, qc.w};
                 const uint32_t sw = (c >> 1) == 0 ? hdr.x : (c >> 1) == 1 ? hdr.y : (c >> 1) == 2 ? hdr.z : hdr.w;
                 const int sc = (int)(int8_t)(sw >> (8 * (2 * (c & 1) + half)));
 #pragma unroll
-                for (int j = 0; j < 4; j++) q6_digits((uint32_t)b[4 * half + j], sc, p1[j], p0[j]);
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t b = ((q4[j] >> (4 * half)) & 0x0F0F0F0Fu) | (((qhw >> (2 * j)) & 0x03030303u) << 4);
+                    q6_digits(b, sc, p1[j], p0[j]);
+                }
             }
             const v4i b0 = {(int)p0[0], (int)p0[1], (int)p0[2], (int)p0[3]};
             const v4i b1 = {(int)p1[0], (int)p1[1], (int)p1[2], (int)p1[3]};
