@@ -707,10 +707,11 @@ hipError_t launch_group_r(int cpl, const WGroup& g, const float* x, hipStream_t 
 }
 
 // m == 1 over a weight group: chunks per lane cover the row in one pass up
-// to K = 16384.  Rows per wavefront: R = 2 once one 16-wavefront workgroup
-// per CU no longer covers the loaded rows with R = 1 (fewer workgroups
-// quantize the activation fewer times; R = 4 measured slower), within the
-// register bound.  XNQ_MV_STREAM_ROWS=1|2 forces R (tuning).  Returns
+// to K = 16384.  One row (GATE: one row of each weight) per wavefront: with
+// the weight loads issued ahead of the quantizer, that measured fastest
+// (decode step 1432 -> 1376 us against two rows per wavefront, which uses
+// fewer workgroups and so quantizes the activation fewer times).
+// XNQ_MV_STREAM_ROWS=2 forces two rows (tuning).  Returns
 // hipErrorNotSupported for a GATE shape past the register bound.
 template <int DT, bool GATE>
 hipError_t launch_group(const WGroup& g, const float* x, hipStream_t s) {
@@ -718,11 +719,7 @@ hipError_t launch_group(const WGroup& g, const float* x, hipStream_t s) {
     const int cpl = (int)std::min<uint32_t>(8, (nchunks + 63) / 64);
     if (GATE && cpl > 5) return hipErrorNotSupported;
     static const int forced = env_int("XNQ_MV_STREAM_ROWS", 0);
-    int ncu = 1;
-    (void)wg_per_cu(reinterpret_cast<const void*>(group_kernel<DT, 1, 1, 16, false>), 1024, 0, &ncu);
-    const uint32_t waves = (uint32_t)ncu * 16;
-    const uint32_t loaded = GATE ? 2 * g.rows : g.rows;
-    int r = forced == 1 || forced == 2 ? forced : (loaded <= waves ? 1 : 2);
+    int r = forced == 2 ? 2 : 1;
     if (cpl > (GATE ? 2 : 5)) r = 1;
     if (r == 1) return launch_group_r<DT, 1, GATE>(cpl, g, x, s);
     return launch_group_r<DT, 2, GATE>(cpl, g, x, s);
