@@ -262,7 +262,7 @@ def _silu(v):
 
 @pytest.mark.parametrize("dt", WEIGHT_DTYPES)
 @pytest.mark.parametrize("m,k,n", [(1, 2048, 300), (1, 4096, 1000), (3, 2048, 300), (1, 12288, 96), (9, 1024, 64),
-                                   (16, 4096, 512), (80, 1024, 256)])
+                                   (16, 4096, 512), (16, 2048, 300), (80, 1024, 256)])
 def test_silu_gate(orc, dev, dt, m, k, n):
     """SwiGLU of llama.rs:258-264: silu(x . gate) * (x . up), one kernel at m = 1;
     above, one shared activation quantize then a matmul per weight (skinny
@@ -282,7 +282,7 @@ def test_silu_gate(orc, dev, dt, m, k, n):
 
 @pytest.mark.parametrize("dt", WEIGHT_DTYPES)
 @pytest.mark.parametrize("m,ns", [(1, (300,)), (1, (512, 128, 128)), (1, (40, 7)), (2, (200, 64, 64)),
-                                  (16, (512, 128, 128)), (80, (256, 64))])
+                                  (16, (512, 128, 128)), (16, (200, 72, 40)), (40, (300, 96)), (80, (256, 64))])
 def test_matmul_group(orc, dev, dt, m, ns):
     """q, k, v projections of one activation (llama.rs:156-158) in one launch."""
     from xn_amd.quantized import matmul_t_group
