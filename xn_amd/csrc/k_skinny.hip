@@ -404,25 +404,26 @@ hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t 
 }  // namespace
 
 // Wavefronts per workgroup (32 columns each): 8 (two per SIMD, so one
-// wavefront's expansion overlaps the other's waits) where the column tiles
-// still cover the CUs with K split at most 4 ways, else 4.  XNQ_SKINNY_NW=4|8
-// forces it (tuning).
-static int skinny_waves(size_t n, size_t k) {
+// wavefront's expansion overlaps the other's waits) above 32 rows (two row
+// tiles: 4096 x 4096 at m = 64 13.8 against 16.2 us) or where the column
+// tiles still cover the CUs with K split at most 4 ways, else 4.
+// XNQ_SKINNY_NW=4|8 forces it (tuning).
+static int skinny_waves(size_t m, size_t n, size_t k) {
     static const int forced = [] {
         const char* e = getenv("XNQ_SKINNY_NW");
         return e ? atoi(e) : 0;
     }();
     if (forced == 4 || forced == 8) return forced;
+    if (m > 32) return 8;
     const size_t tiles8 = (n + 255) / 256, nsb = k / 256;
     return tiles8 * std::min<size_t>(4, nsb / 2) >= 200 ? 8 : 4;
 }
 
 uint32_t skinny_splits(size_t m, size_t n, size_t k) {
-    (void)m;
     // the LDS ring takes most of a CU, so one workgroup per CU: split K while
     // the grid still fits the 256 CUs at once, each split at least two
     // super-blocks long
-    const size_t tiles = (n + 32 * skinny_waves(n, k) - 1) / (32 * skinny_waves(n, k));
+    const size_t tiles = (n + 32 * skinny_waves(m, n, k) - 1) / (32 * skinny_waves(m, n, k));
     const size_t nsb = k / 256;
     size_t splits = 256 / tiles;
     if (splits > nsb / 2) splits = nsb / 2;
@@ -442,7 +443,7 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
     if (splits > 1 && !partial) splits = 1;
     size_t n = 0;
     for (uint32_t t = 0; t < G.count; t++) n += G.w[t].n;
-    const bool w8 = skinny_waves(n, G.w[0].k) == 8;
+    const bool w8 = skinny_waves(m, n, G.w[0].k) == 8;
 #define XNQ_SK(DT)                                                                                   \
     if (G.w[0].dtype == DT) {                                                                        \
         if (m <= 32)                                                                                 \
