@@ -729,9 +729,9 @@ inline int pick_cpl(uint32_t nchunks) {
     return nchunks <= 64 ? 1 : nchunks <= 128 ? 2 : nchunks <= 256 ? 4 : 8;
 }
 
-// Decode kernels read a quantized workspace (4 wavefronts per workgroup,
-// many workgroups); the fused m == 1 kernel quantizes in LDS and so uses
-// 16-wavefront workgroups to share that work.
+// Decode kernels read a quantized workspace (4 wavefronts per workgroup at
+// one row, 8 at 2..8 rows; many workgroups); the fused m == 1 kernel
+// quantizes in LDS and so uses 16-wavefront workgroups to share that work.
 template <int DT, int MB, bool FUSED>
 hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const float* x, uint32_t m0,
                       uint32_t mc, float* y, hipStream_t s) {
@@ -757,6 +757,18 @@ hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const floa
         XNQ_MV(1, 1) XNQ_MV(2, 1) XNQ_MV(4, 1) XNQ_MV(1, 2) XNQ_MV(2, 2) XNQ_MV(4, 2)
         XNQ_MV(1, 4) XNQ_MV(2, 4) XNQ_MV(1, 8)
     } else {
+        // 2..8 rows: 8-wavefront workgroups stage the rows into LDS half as
+        // often as 4-wavefront ones (4096 -> 14336 at m = 4: 11.9 against
+        // 12.5 us); XNQ_MV_NW_MB=4 restores 4 (tuning)
+        if constexpr (!FUSED) {
+            static const int nw = env_int("XNQ_MV_NW_MB", 8);
+            if (R == 1 && nw == 8) {
+                if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
+                if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
+                if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
+                if (cpl == 8) return launch_one<DT, MB, 1, 8, 8, FUSED>(w, a, x, m0, mc, y, s);
+            }
+        }
         XNQ_MV(1, 1) XNQ_MV(1, 2) XNQ_MV(1, 4) XNQ_MV(1, 8)
     }
 #undef XNQ_MV
