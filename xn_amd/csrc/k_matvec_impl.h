@@ -730,7 +730,7 @@ inline int pick_cpl(uint32_t nchunks) {
 }
 
 // Decode kernels read a quantized workspace (4 wavefronts per workgroup at
-// one row, 8 at 2..8 rows; many workgroups); the fused m == 1 kernel
+// one row of K <= 8192, else 8; many workgroups); the fused m == 1 kernel
 // quantizes in LDS and so uses 16-wavefront workgroups to share that work.
 template <int DT, int MB, bool FUSED>
 hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const float* x, uint32_t m0,
@@ -747,6 +747,19 @@ hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const floa
             if (cpl == 8) return launch_one<DT, MB, 1, 8, 4, FUSED>(w, a, x, m0, mc, y, s);
         }
         if (R == 1 && fnw == 8) {
+            if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
+            if (cpl == 8) return launch_one<DT, MB, 1, 8, 8, FUSED>(w, a, x, m0, mc, y, s);
+        }
+    }
+    if constexpr (MB == 1 && !FUSED) {
+        // rows of 8 chunks per lane (K > 8192): 8-wavefront workgroups
+        // (14336 -> 4096 Q4_K 8.25 against 8.87 us, Q4_0 7.97 against 8.97);
+        // shorter rows keep 4 (8192 -> 28672: 22.5 against 23.3).
+        // XNQ_MV_NW1=4|8 forces it (tuning).
+        static const int nw1 = env_int("XNQ_MV_NW1", 0);
+        if (R == 1 && (nw1 == 8 || (nw1 == 0 && cpl == 8))) {
             if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
             if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
             if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
