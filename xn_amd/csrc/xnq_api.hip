@@ -400,8 +400,8 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
 }
 
 // Automatic routes (measured on MI355X):
-//   m < 12 (m < 8 when k >= 8192,
-//   m < 6 for Q4K with n >= 8192)   matvec kernels (up to 8 rows per launch)
+//   m <= 8 (Q4K: m < 6 when
+//   n >= 8192, m < 8 when k >= 8192) matvec kernels (up to 8 rows per launch)
 //   m <= 64                          skinny int8-MFMA kernel for Q4K / Q6K
 //   larger m                         tiled int8-MFMA prefill kernel
 // Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MAX_ROWS and
@@ -415,10 +415,17 @@ static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k) {
     if (forced == 1) return kMatvec;
     if (forced == 2) return kMfma;
     if (forced == 3) return kSkinny;
-    // measured crossovers: the matvec kernels' cost grows with every row, the
-    // skinny kernel's hardly at all below 32 rows
-    const size_t skinny_lo =
-        skinny_min ? skinny_min : (dtype == XNQ_Q4K && n >= 8192) ? 6 : (k >= 8192 ? 8 : 12);
+    // measured crossovers: the matvec kernels' cost grows with every row and
+    // past 8 rows takes a second launch, the skinny kernel's hardly grows
+    // below 32 rows (4096 x 4096: matvec 8.5 us at m = 8, 12.8 at m = 10,
+    // skinny 10.0 at both; 14336 -> 4096 Q6_K: 23.5 against 26.6 at m = 8;
+    // 4096 -> 14336 Q4_K: 21.3 against 17.7 at m = 6; 14336 -> 4096 Q4_K,
+    // whose skinny expansion is cheaper than Q6_K's: 20.1 against 18.9 at m = 8)
+    const size_t skinny_lo = skinny_min               ? skinny_min
+                             : dtype != XNQ_Q4K        ? 9
+                             : n >= 8192               ? 6
+                             : k >= 8192               ? 8
+                                                       : 9;
     if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
     if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
     return kMatvec;
