@@ -161,7 +161,7 @@ def test_matmul_small(orc, dev, dt, m, entry):
     (Q4K, 14336, 4096),
     (Q6K, 14336, 4096),   # config 5 FFN down
 ])
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 8])  # m = 8: matvec for Q6_K and 4096 x 4096, skinny for Q4_K K = 14336
 def test_matmul_config_shapes(orc, dev, dt, k, n, m):
     rng = np.random.default_rng(7000 + dt + k + n + m)
     w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
