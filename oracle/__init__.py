@@ -65,6 +65,12 @@ def lib() -> ctypes.CDLL:
         L.orc_make_qkx1_quants.argtypes = [i, i, vp, i, vp]
         L.orc_make_qx_quants.restype = ctypes.c_float
         L.orc_make_qx_quants.argtypes = [i, i, vp, vp, i]
+        L.orc_make_qkx1_quants_ex.restype = ctypes.c_float
+        L.orc_make_qkx1_quants_ex.argtypes = [i, i, vp, i, vp, vp, vp]
+        L.orc_make_qx_quants_ex.restype = ctypes.c_float
+        L.orc_make_qx_quants_ex.argtypes = [i, i, vp, vp, i, vp]
+        L.orc_make_q3_quants_ex.restype = ctypes.c_float
+        L.orc_make_q3_quants_ex.argtypes = [vp, i, i, i, vp, vp]
         L.cpu_pool_init.restype = i
         L.cpu_pool_init.argtypes = [sz]
         L.cpu_matmul.restype = i
@@ -194,6 +200,38 @@ def block_ints(dt: int, w_blocks: np.ndarray, a_blocks: np.ndarray, m: int, n: i
         wq = np.concatenate([(qs & 0xF) - 8, (qs >> 4) - 8], axis=2)
     out[..., 0] = np.einsum("mbe,nbe->mnb", aq, wq)
     return out
+
+
+def make_qkx1_quants(nmax: int, ntry: int, x) -> tuple:
+    """utils.rs:205-254 -> (scale, -min, levels of the last pass,
+    passes run, iscale and min that pass assigned the levels with)."""
+    x = _f32(x).reshape(-1)
+    nm = np.zeros(1, np.float32)
+    lv = np.zeros(x.size, np.uint8)
+    info = np.zeros(3, np.float32)
+    s = lib().orc_make_qkx1_quants_ex(nmax, ntry, x.ctypes.data, x.size, nm.ctypes.data, lv.ctypes.data,
+                                      info.ctypes.data)
+    return np.float32(s), nm[0], lv, int(info[0]), info[1], info[2]
+
+
+def make_qx_quants(nmax: int, x, rmse_type: int) -> tuple:
+    """utils.rs:65-202 -> (scale, levels (stored, 0..2*nmax-1), info:
+    [whole-block passes, per-element passes, changes in the last pass])."""
+    x = _f32(x).reshape(-1)
+    ls = np.zeros(x.size, np.int8)
+    info = np.zeros(3, np.int32)
+    s = lib().orc_make_qx_quants_ex(x.size, nmax, x.ctypes.data, ls.ctypes.data, rmse_type, info.ctypes.data)
+    return np.float32(s), ls, info
+
+
+def make_q3_quants(nmax: int, x, do_rmse: bool) -> tuple:
+    """utils.rs:257-322 -> (scale, levels (stored, 0..2*nmax-1), info:
+    [per-element passes, changes in the last pass])."""
+    x = _f32(x).reshape(-1)
+    ls = np.zeros(x.size, np.int8)
+    info = np.zeros(2, np.int32)
+    s = lib().orc_make_q3_quants_ex(x.ctypes.data, x.size, nmax, int(do_rmse), ls.ctypes.data, info.ctypes.data)
+    return np.float32(s), ls, info
 
 
 def cpu_pool_init(threads: int) -> int:

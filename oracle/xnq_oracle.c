@@ -317,17 +317,28 @@ static int32_t total_key(float f) {
     return i ^ (int32_t)(((uint32_t)(i >> 31)) >> 1);
 }
 
-/* utils.rs:205-254 make_qkx1_quants; returns scale, writes -min to *neg_min. */
-float orc_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* neg_min) {
+/* utils.rs:205-254 make_qkx1_quants; returns scale, writes -min to *neg_min.
+ * The _ex form also reports, for the tests that pin it, the levels of the
+ * last pass (lout, n bytes) and info[3] = {passes run, the iscale and the min
+ * that pass assigned the levels with}; both may be NULL. */
+float orc_make_qkx1_quants_ex(int nmax, int ntry, const float* x, int n, float* neg_min, uint8_t* lout,
+                              float* info) {
     uint8_t l[QK_K];
     memset(l, 0, sizeof l);
+    int passes = 0;
+    float iscale_used = 0.0f, min_used = 0.0f;
     /* min_by keeps the first minimum, max_by keeps the last maximum */
     float mn = x[0], mx = x[0];
     for (int i = 1; i < n; i++) {
         if (total_key(x[i]) < total_key(mn)) mn = x[i];
         if (total_key(x[i]) >= total_key(mx)) mx = x[i];
     }
-    if (mx == mn) { *neg_min = 0.0f; return 0.0f; }
+    if (mx == mn) {
+        *neg_min = 0.0f;
+        if (lout) memset(lout, 0, (size_t)n);
+        if (info) info[0] = info[1] = info[2] = 0.0f;
+        return 0.0f;
+    }
     float min = rmin(mn, 0.0f);
     float iscale = (float)nmax / (mx - min);
     float scale = 1.0f / iscale;
@@ -335,6 +346,9 @@ float orc_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* neg
         float sumlx = 0.0f;
         int32_t suml2 = 0;
         int did_change = 0;
+        passes = t + 1;
+        iscale_used = iscale;
+        min_used = min;
         for (int i = 0; i < n; i++) {
             float value = x[i];
             int32_t li = clampi(nearest_int(iscale * (value - min)), 0, nmax);
@@ -352,7 +366,13 @@ float orc_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* neg
         if (!did_change) break;
     }
     *neg_min = -min;
+    if (lout) memcpy(lout, l, (size_t)n);
+    if (info) { info[0] = (float)passes; info[1] = iscale_used; info[2] = min_used; }
     return scale;
+}
+
+float orc_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* neg_min) {
+    return orc_make_qkx1_quants_ex(nmax, ntry, x, n, neg_min, NULL, NULL);
 }
 
 /* k_quants.rs:1418-1473 BlockQ4K::from_float */
@@ -515,8 +535,12 @@ float orc_q4k_vec_dot(size_t n, const void* xv, const void* yv) {
 
 /* ------------------------------------------------------------ Q6_K */
 
-/* utils.rs:65-202 make_qx_quants */
-float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_type) {
+/* utils.rs:65-202 make_qx_quants.  The _ex form also reports, for the tests
+ * that pin it, info[3] = {passes of the first (whole-block) refinement loop,
+ * passes of the per-element loop, elements the last per-element pass
+ * changed}; info may be NULL. */
+float orc_make_qx_quants_ex(int n, int nmax, const float* x, int8_t* ls, int rmse_type, int32_t* info) {
+    if (info) info[0] = info[1] = info[2] = 0;
     float max = 0.0f, amax = 0.0f;
     for (int i = 0; i < n; i++) {
         float ax = fabsf(x[i]);
@@ -548,6 +572,7 @@ float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_t
     float scale = sumlx / suml2;
     float best = scale * sumlx;
     for (int itry = 0; itry < 3; itry++) {
+        if (info) info[0] = itry + 1;
         float is2 = 1.0f / scale;
         float slx = 0.0f, sl2 = 0.0f;
         int changed = 0;
@@ -572,6 +597,7 @@ float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_t
     }
     for (int itry = 0; itry < 5; itry++) {
         int n_changed = 0;
+        if (info) info[1] = itry + 1;
         for (int i = 0; i < n; i++) {
             float xi = x[i];
             float w = weight_type == 1 ? xi * xi : 1.0f;
@@ -594,6 +620,7 @@ float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_t
                 }
             }
         }
+        if (info) info[2] = n_changed;
         if (n_changed == 0) break;
     }
     if (rmse_type < 3) return scale;
@@ -619,6 +646,10 @@ float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_t
         }
     }
     return scale;
+}
+
+float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_type) {
+    return orc_make_qx_quants_ex(n, nmax, x, ls, rmse_type, NULL);
 }
 
 /* k_quants.rs:1801-1871 BlockQ6K::from_float */

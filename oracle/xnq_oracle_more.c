@@ -392,8 +392,11 @@ float orc_q2k_vec_dot(size_t n, const void* xv, const void* yv) {
 
 /* ------------------------------------------------------------ Q3_K */
 
-/* utils.rs:257-320 make_q3_quants */
-float orc_make_q3_quants(const float* x, int n, int nmax, int do_rmse, int8_t* lout) {
+/* utils.rs:257-320 make_q3_quants.  The _ex form also reports, for the tests
+ * that pin it, info[2] = {passes of the per-element loop, elements its last
+ * pass changed}; info may be NULL. */
+float orc_make_q3_quants_ex(const float* x, int n, int nmax, int do_rmse, int8_t* lout, int32_t* info) {
+    if (info) info[0] = info[1] = 0;
     int8_t l[QK_K];
     memset(l, 0, sizeof l);
     float max = 0.0f, amax = 0.0f;
@@ -417,6 +420,7 @@ float orc_make_q3_quants(const float* x, int n, int nmax, int do_rmse, int8_t* l
         }
         for (int it = 0; it < 5; it++) {
             int n_changed = 0;
+            if (info) info[0] = it + 1;
             for (int i = 0; i < n; i++) {
                 float w = x[i] * x[i];
                 float slx = sumlx - w * x[i] * (float)l[i];
@@ -435,6 +439,7 @@ float orc_make_q3_quants(const float* x, int n, int nmax, int do_rmse, int8_t* l
                     }
                 }
             }
+            if (info) info[1] = n_changed;
             if (n_changed == 0) break;
         }
         for (int i = 0; i < n; i++) l[i] = (int8_t)(l[i] + nmax);
@@ -447,6 +452,10 @@ float orc_make_q3_quants(const float* x, int n, int nmax, int do_rmse, int8_t* l
     }
     if (lout) memcpy(lout, l, (size_t)n);
     return 1.0f / iscale;
+}
+
+float orc_make_q3_quants(const float* x, int n, int nmax, int do_rmse, int8_t* lout) {
+    return orc_make_q3_quants_ex(x, n, nmax, do_rmse, lout, NULL);
 }
 
 /* The 16 six-bit scales of a Q3K block (the aux/KMASK shuffle of
