@@ -582,12 +582,9 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
 template <int DT>
 hipError_t launch_dt(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                      hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(qmm_kernel<DT>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, Lay<DT>::kLds);
+    {
+        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(qmm_kernel<DT>), Lay<DT>::kLds);
         if (e != hipSuccess) return e;
-        attr = true;
     }
     const uint32_t nsb = w.k / 256;
     const uint32_t per = (nsb + splits - 1) / splits;

@@ -366,12 +366,9 @@ hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t 
                             hipStream_t s) {
     using L = KLay<DT, MT, NW>;
     constexpr int kCols = L::kCols;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(skinny_kernel<DT, MT, NW>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
+    {
+        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(skinny_kernel<DT, MT, NW>), L::kLds);
         if (e != hipSuccess) return e;
-        attr = true;
     }
     const uint32_t nsb = G.w[0].k / 256;
     const uint32_t per = (nsb + splits - 1) / splits;

@@ -7,7 +7,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "xnq_internal.h"
 
@@ -201,6 +204,19 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
     return true;
 }
 
+hipError_t set_max_lds(const void* kernel, int bytes) {
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({kernel, dev})) return hipSuccess;
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) done.insert({kernel, dev});
+    return e;
+}
+
 static size_t env_size(const char* name, size_t dflt) {
     const char* e = getenv(name);
     return e ? (size_t)strtoull(e, nullptr, 10) : dflt;
@@ -214,21 +230,23 @@ size_t skinny_max_rows() {
 // Whether the prefill (tiled MFMA) route can be taken for m activation rows,
 // in which case the activation quantizer also writes the row-tiled image.
 // It depends on m and the forced route, not on n, so xnq_quantize_lhs (which
-// has no n) and the matmul agree; xnq_set_route must not change between them.
-bool tiled_act(uint32_t weight_dtype, size_t m, size_t k) {
-    const int forced = g_route.load();
+// has no n) and the matmul agree.  `forced` is the route override as read
+// once at the public entry point, so sizing and launching within one call
+// always agree; between separate quantize_lhs and matmul_preq calls
+// xnq_set_route must not change.
+static bool tiled_act(uint32_t weight_dtype, size_t m, size_t k, int forced) {
     if (forced == 1 || forced == 3) return false;
     return mfma_supported(weight_dtype, m, 0, k) && (forced == 2 || m > skinny_max_rows());
 }
 
-ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k) {
+ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k, int forced) {
     ALayout L;
     L.act_dtype = vec_dot_type(weight_dtype);
     L.m = m;
     L.k = k;
     L.img = act_img((uint32_t)k, L.act_dtype == XNQ_Q8K);  // Q8_1 uses the Q8_0 image
     L.bytes = align_up(m * L.img.row_bytes);
-    if (tiled_act(weight_dtype, m, k)) {
+    if (tiled_act(weight_dtype, m, k, forced)) {
         L.tiled = true;
         L.tile_off = L.bytes;
         L.tile = tile_img(m, (uint32_t)k);
@@ -352,7 +370,7 @@ size_t xnq_qtensor_device_bytes(const xnq_qtensor* qt) { return qt ? qt->L.bytes
 
 size_t xnq_lhs_workspace_size(uint32_t weight_dtype, size_t m, size_t k) {
     if (!device_dtype(weight_dtype)) return 0;
-    return act_layout(weight_dtype, m, k).bytes;
+    return act_layout(weight_dtype, m, k, g_route.load()).bytes;
 }
 
 static xnq_status check_lhs(uint32_t weight_dtype, size_t k) {
@@ -364,18 +382,23 @@ static xnq_status check_lhs(uint32_t weight_dtype, size_t k) {
     return XNQ_OK;
 }
 
-xnq_status xnq_quantize_lhs(uint32_t weight_dtype, size_t m, size_t k, const float* lhs_dev,
-                            void* workspace_dev, void* stream) {
+static xnq_status quantize_lhs_impl(uint32_t weight_dtype, size_t m, size_t k, const float* lhs_dev,
+                                    void* workspace_dev, void* stream, int forced) {
     if (!device_dtype(weight_dtype))
         return fail(XNQ_ERR_UNSUPPORTED, "no device activation quantizer for dtype %u", weight_dtype);
     xnq_status st = check_lhs(weight_dtype, k);
     if (st) return st;
     if (m == 0) return XNQ_OK;
     if (!lhs_dev || !workspace_dev) return fail(XNQ_ERR_INVALID, "null pointer");
-    const ALayout A = act_layout(weight_dtype, m, k);
+    const ALayout A = act_layout(weight_dtype, m, k, forced);
     hipError_t e = launch_quantize_act(A, lhs_dev, workspace_dev, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "quantize_lhs");
     return XNQ_OK;
+}
+
+xnq_status xnq_quantize_lhs(uint32_t weight_dtype, size_t m, size_t k, const float* lhs_dev,
+                            void* workspace_dev, void* stream) {
+    return quantize_lhs_impl(weight_dtype, m, k, lhs_dev, workspace_dev, stream, g_route.load());
 }
 
 xnq_status xnq_set_route(int route) {
@@ -404,14 +427,14 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
 //   n >= 8192, m < 8 when k >= 8192) matvec kernels (up to 8 rows per launch)
 //   m <= 64                          skinny int8-MFMA kernel for Q4K / Q6K
 //   larger m                         tiled int8-MFMA prefill kernel
-// Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MAX_ROWS and
-// XNQ_MFMA_MIN_ROWS override the crossovers for tuning.
+// Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MIN_ROWS and
+// XNQ_SKINNY_MAX_ROWS override the skinny range for tuning (read once per
+// process); `forced` is xnq_set_route's override as read at the entry point.
 enum Route { kMatvec, kSkinny, kMfma };
 
-static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k) {
+static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced) {
     static const size_t skinny_min = env_size("XNQ_SKINNY_MIN_ROWS", 0);
     const size_t skinny_max = skinny_max_rows();
-    const int forced = g_route.load();
     if (forced == 1) return kMatvec;
     if (forced == 2) return kMfma;
     if (forced == 3) return kSkinny;
@@ -432,8 +455,8 @@ static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k) {
 }
 
 // Split-K partial sums sit after the activation image in the workspace.
-static size_t partial_offset(uint32_t dtype, size_t m, size_t k) {
-    return (act_layout(dtype, m, k).bytes + kAlign - 1) / kAlign * kAlign;
+static size_t partial_offset(uint32_t dtype, size_t m, size_t k, int forced) {
+    return (act_layout(dtype, m, k, forced).bytes + kAlign - 1) / kAlign * kAlign;
 }
 
 static uint32_t route_splits(Route r, size_t m, size_t n, size_t k) {
@@ -442,18 +465,21 @@ static uint32_t route_splits(Route r, size_t m, size_t n, size_t k) {
     return 1;
 }
 
-size_t xnq_qtensor_workspace_size(const xnq_qtensor* qt, size_t m) {
+static size_t workspace_size_impl(const xnq_qtensor* qt, size_t m, int forced) {
     if (!qt) return 0;
     const size_t k = qt->L.k, n = qt->L.n;
-    size_t bytes = act_layout(qt->L.dtype, m, k).bytes;
-    const uint32_t splits = route_splits(pick_route(qt->L.dtype, m, n, k), m, n, k);
-    if (splits > 1) bytes = partial_offset(qt->L.dtype, m, k) + (size_t)splits * m * n * sizeof(float);
+    size_t bytes = act_layout(qt->L.dtype, m, k, forced).bytes;
+    const uint32_t splits = route_splits(pick_route(qt->L.dtype, m, n, k, forced), m, n, k);
+    if (splits > 1) bytes = partial_offset(qt->L.dtype, m, k, forced) + (size_t)splits * m * n * sizeof(float);
     return bytes;
 }
 
-xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
-                                   const void* workspace_dev, size_t workspace_bytes, float* dst_dev,
-                                   void* stream) {
+size_t xnq_qtensor_workspace_size(const xnq_qtensor* qt, size_t m) {
+    return workspace_size_impl(qt, m, g_route.load());
+}
+
+static xnq_status matmul_preq_impl(const xnq_qtensor* qt, size_t m, size_t k, size_t n, const void* workspace_dev,
+                                   size_t workspace_bytes, float* dst_dev, void* stream, int forced) {
     xnq_status st = check_mkn(qt, m, k, n);
     if (st) return st;
     if (m == 0 || n == 0) return XNQ_OK;
@@ -461,14 +487,14 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     const WView w = make_wview(qt->L, qt->buf);
-    const AView a = make_aview(act_layout(qt->L.dtype, m, k), workspace_dev);
+    const AView a = make_aview(act_layout(qt->L.dtype, m, k, forced), workspace_dev);
     hipError_t e;
-    const Route r = pick_route(qt->L.dtype, m, n, k);
+    const Route r = pick_route(qt->L.dtype, m, n, k, forced);
     if (r == kMfma || r == kSkinny) {
         if (r == kMfma ? !mfma_supported(qt->L.dtype, m, n, k) : !skinny_supported(qt->L.dtype, m, n, k))
             return fail(XNQ_ERR_UNSUPPORTED, "no MFMA kernel for this dtype/shape");
         uint32_t splits = route_splits(r, m, n, k);
-        const size_t off = partial_offset(qt->L.dtype, m, k);
+        const size_t off = partial_offset(qt->L.dtype, m, k, forced);
         if (off + (size_t)splits * m * n * sizeof(float) > workspace_bytes) splits = 1;
         float* partial = splits > 1 ? reinterpret_cast<float*>((uint8_t*)workspace_dev + off) : nullptr;
         e = r == kMfma ? launch_mfma(w, a, m, splits, dst_dev, partial, (hipStream_t)stream)
@@ -480,6 +506,12 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
         return fail(XNQ_ERR_INVALID, "k = %zu is too large for the matvec kernel's LDS", k);
     if (e != hipSuccess) return hip_fail(e, "matmul kernel");
     return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                   const void* workspace_dev, size_t workspace_bytes, float* dst_dev,
+                                   void* stream) {
+    return matmul_preq_impl(qt, m, k, n, workspace_dev, workspace_bytes, dst_dev, stream, g_route.load());
 }
 
 // Decode: the fused matvec route quantizes the activation row in LDS inside
@@ -506,20 +538,25 @@ static size_t fused_max_k() {
 // `grouped`: the weight is one of a q/k/v group or a gate/up pair, whose
 // one-launch kernels take K <= XNQ_FUSED_MAX_K at any N; a single matmul_t
 // takes the element limit alone.
-static bool fused_route(const xnq_qtensor* qt, size_t m, bool grouped = false) {
-    const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k);
+static bool fused_route(const xnq_qtensor* qt, size_t m, int forced, bool grouped = false) {
+    const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k, forced);
     if (r != kMatvec) return false;
-    if (g_route.load() == 1) return true;
+    if (forced == 1) return true;
     return m == 1 && ((grouped && qt->L.k <= fused_max_k()) || qt->L.n * qt->L.k <= fused_max_elems());
 }
 
-size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m) {
-    if (!qt || fused_route(qt, m)) return 0;
-    return xnq_qtensor_workspace_size(qt, m);
+static size_t matmul_t_workspace_size_impl(const xnq_qtensor* qt, size_t m, int forced) {
+    if (!qt || fused_route(qt, m, forced)) return 0;
+    return workspace_size_impl(qt, m, forced);
 }
 
-xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, size_t n, const float* lhs_dev,
-                                   void* workspace_dev, size_t workspace_bytes, float* dst_dev, void* stream) {
+size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m) {
+    return matmul_t_workspace_size_impl(qt, m, g_route.load());
+}
+
+static xnq_status matmul_t_ws_impl(const xnq_qtensor* qt, size_t m, size_t k, size_t n, const float* lhs_dev,
+                                   void* workspace_dev, size_t workspace_bytes, float* dst_dev, void* stream,
+                                   int forced) {
     xnq_status st = check_mkn(qt, m, k, n);
     if (st) return st;
     st = check_lhs(qt->L.dtype, k);
@@ -529,7 +566,7 @@ xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, si
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
-    if (fused_route(qt, m)) {
+    if (fused_route(qt, m, forced)) {
         const WView w = make_wview(qt->L, qt->buf);
         hipError_t e = launch_matvec_fused(w, lhs_dev, m, dst_dev, s);
         if (e == hipErrorInvalidConfiguration)
@@ -537,21 +574,28 @@ xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, si
         if (e != hipSuccess) return hip_fail(e, "matvec kernel");
         return XNQ_OK;
     }
-    const size_t need = act_layout(qt->L.dtype, m, k).bytes;
+    const size_t need = act_layout(qt->L.dtype, m, k, forced).bytes;
     if (!workspace_dev || workspace_bytes < need)
         return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu the activation needs",
                     workspace_bytes, need);
-    st = xnq_quantize_lhs(qt->L.dtype, m, k, lhs_dev, workspace_dev, stream);
-    if (!st) st = xnq_qtensor_matmul_preq(qt, m, k, n, workspace_dev, workspace_bytes, dst_dev, stream);
+    st = quantize_lhs_impl(qt->L.dtype, m, k, lhs_dev, workspace_dev, stream, forced);
+    if (!st) st = matmul_preq_impl(qt, m, k, n, workspace_dev, workspace_bytes, dst_dev, stream, forced);
     return st;
+}
+
+xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, size_t n, const float* lhs_dev,
+                                   void* workspace_dev, size_t workspace_bytes, float* dst_dev, void* stream) {
+    return matmul_t_ws_impl(qt, m, k, n, lhs_dev, workspace_dev, workspace_bytes, dst_dev, stream, g_route.load());
 }
 
 xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
                                 const float* lhs_dev, float* dst_dev, void* stream) {
     xnq_status st = check_mkn(qt, m, k, n);
     if (st) return st;
-    const size_t ws_bytes = xnq_qtensor_matmul_t_workspace_size(qt, m);
-    if (ws_bytes == 0 || n == 0 || m == 0) return xnq_qtensor_matmul_t_ws(qt, m, k, n, lhs_dev, nullptr, 0, dst_dev, stream);
+    const int forced = g_route.load();
+    const size_t ws_bytes = matmul_t_workspace_size_impl(qt, m, forced);
+    if (ws_bytes == 0 || n == 0 || m == 0)
+        return matmul_t_ws_impl(qt, m, k, n, lhs_dev, nullptr, 0, dst_dev, stream, forced);
     DeviceGuard g(qt->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
@@ -564,7 +608,7 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, ws_bytes, s);
     if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(workspace)");
-    st = xnq_qtensor_matmul_t_ws(qt, m, k, n, lhs_dev, ws, ws_bytes, dst_dev, stream);
+    st = matmul_t_ws_impl(qt, m, k, n, lhs_dev, ws, ws_bytes, dst_dev, stream, forced);
     (void)hipFreeAsync(ws, s);
     return st;
 }
@@ -574,10 +618,10 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
 
 // The grouped m == 1 kernel takes the group when every weight is on the
 // fused decode route with one dtype, one K and one device.
-static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m) {
+static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
     if (m != 1 || count == 0 || count > (size_t)kMaxGroup) return false;
     for (size_t i = 0; i < count; i++) {
-        if (!qts[i] || !fused_route(qts[i], m, true)) return false;
+        if (!qts[i] || !fused_route(qts[i], m, forced, true)) return false;
         if (qts[i]->L.dtype != qts[0]->L.dtype || qts[i]->L.k != qts[0]->L.k || qts[i]->device != qts[0]->device)
             return false;
     }
@@ -587,10 +631,10 @@ static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m) {
 // Off the one-launch route, weights of one dtype, K and device that all
 // take a quantized workspace share one quantize launch: the activation image
 // depends only on the dtype, m and K.
-static bool shared_quantize(const xnq_qtensor* const* qts, size_t count, size_t m) {
+static bool shared_quantize(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
     if (count < 2) return false;
     for (size_t i = 0; i < count; i++) {
-        if (!qts[i] || fused_route(qts[i], m)) return false;
+        if (!qts[i] || fused_route(qts[i], m, forced)) return false;
         if (qts[i]->L.dtype != qts[0]->L.dtype || qts[i]->L.k != qts[0]->L.k || qts[i]->device != qts[0]->device)
             return false;
     }
@@ -599,11 +643,11 @@ static bool shared_quantize(const xnq_qtensor* const* qts, size_t count, size_t 
 
 // Weights that share one quantize and all take the skinny route run as one
 // skinny launch over their joined column tiles, with one split-K sum.
-static bool skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m) {
-    if (!shared_quantize(qts, count, m)) return false;
+static bool skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
+    if (!shared_quantize(qts, count, m, forced)) return false;
     for (size_t i = 0; i < count; i++) {
         const WLayout& L = qts[i]->L;
-        if (pick_route(L.dtype, m, L.n, L.k) != kSkinny || !skinny_supported(L.dtype, m, L.n, L.k)) return false;
+        if (pick_route(L.dtype, m, L.n, L.k, forced) != kSkinny || !skinny_supported(L.dtype, m, L.n, L.k)) return false;
     }
     return true;
 }
@@ -615,16 +659,16 @@ static size_t joined_n(const xnq_qtensor* const* qts, size_t count) {
 }
 
 // Activation image, then one partial region per weight ([split][m][n_t]).
-static size_t skinny_group_ws(const xnq_qtensor* const* qts, size_t count, size_t m) {
+static size_t skinny_group_ws(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
     const size_t k = qts[0]->L.k, n = joined_n(qts, count);
-    return partial_offset(qts[0]->L.dtype, m, k) + (size_t)skinny_splits(m, n, k) * m * n * sizeof(float);
+    return partial_offset(qts[0]->L.dtype, m, k, forced) + (size_t)skinny_splits(m, n, k) * m * n * sizeof(float);
 }
 
 // Quantize once, then the skinny kernel over the group (silu: gate, up pair
 // into G.y[0]).
 static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
                                    const float* lhs_dev, float* const* dsts, void* workspace_dev,
-                                   size_t workspace_bytes, bool silu, void* stream);
+                                   size_t workspace_bytes, bool silu, void* stream, int forced);
 
 static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* const* dsts) {
     WGroup g{};
@@ -642,33 +686,37 @@ static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* con
 
 static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
                                    const float* lhs_dev, float* const* dsts, void* workspace_dev,
-                                   size_t workspace_bytes, bool silu, void* stream) {
+                                   size_t workspace_bytes, bool silu, void* stream, int forced) {
     const uint32_t dt = qts[0]->L.dtype;
-    const size_t need = skinny_group_ws(qts, count, m);
+    const size_t need = skinny_group_ws(qts, count, m, forced);
     if (!workspace_dev || workspace_bytes < need)
         return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
     DeviceGuard g(qts[0]->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
-    xnq_status st = xnq_quantize_lhs(dt, m, k, lhs_dev, workspace_dev, stream);
+    xnq_status st = quantize_lhs_impl(dt, m, k, lhs_dev, workspace_dev, stream, forced);
     if (st) return st;
     const WGroup G = make_group(qts, count, dsts);
-    const AView a = make_aview(act_layout(dt, m, k), workspace_dev);
-    float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + partial_offset(dt, m, k));
+    const AView a = make_aview(act_layout(dt, m, k, forced), workspace_dev);
+    float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + partial_offset(dt, m, k, forced));
     const hipError_t e = launch_skinny_group(G, a, m, skinny_splits(m, joined_n(qts, count), k), partial, silu,
                                              (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "grouped skinny kernel");
     return XNQ_OK;
 }
 
-size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m) {
+static size_t silu_gate_ws_impl(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, int forced) {
     if (!gate || !up) return 0;
     const xnq_qtensor* pair[2] = {gate, up};
-    if (group_route(pair, 2, m) && gate->L.k <= 64 * 5 * 32) return 0;
-    const size_t a = xnq_qtensor_matmul_t_workspace_size(gate, m), b = xnq_qtensor_matmul_t_workspace_size(up, m);
+    if (group_route(pair, 2, m, forced) && gate->L.k <= 64 * 5 * 32) return 0;
+    const size_t a = matmul_t_workspace_size_impl(gate, m, forced), b = matmul_t_workspace_size_impl(up, m, forced);
     const size_t two = align_up(a > b ? a : b, kAlign) + m * up->L.n * sizeof(float);
-    if (gate->L.n != up->L.n || !skinny_group(pair, 2, m)) return two;
-    const size_t one = skinny_group_ws(pair, 2, m);
+    if (gate->L.n != up->L.n || !skinny_group(pair, 2, m, forced)) return two;
+    const size_t one = skinny_group_ws(pair, 2, m, forced);
     return one > two ? one : two;
+}
+
+size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m) {
+    return silu_gate_ws_impl(gate, up, m, g_route.load());
 }
 
 xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
@@ -681,7 +729,8 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     if (gate->device != up->device) return fail(XNQ_ERR_INVALID, "gate and up live on different devices");
     if (m == 0 || n == 0) return XNQ_OK;
     if (!lhs_dev || !dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
-    const size_t need = xnq_matmul_t_silu_gate_workspace_size(gate, up, m);
+    const int forced = g_route.load();
+    const size_t need = silu_gate_ws_impl(gate, up, m, forced);
     hipStream_t s = (hipStream_t)stream;
     if (need == 0) {
         st = check_lhs(gate->L.dtype, k);
@@ -699,23 +748,23 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     }
     if (!workspace_dev || workspace_bytes < need)
         return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
-    const size_t a = xnq_qtensor_matmul_t_workspace_size(gate, m), b = xnq_qtensor_matmul_t_workspace_size(up, m);
+    const size_t a = matmul_t_workspace_size_impl(gate, m, forced), b = matmul_t_workspace_size_impl(up, m, forced);
     const size_t off = align_up(a > b ? a : b, kAlign);
     float* u = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + off);
     const xnq_qtensor* pair[2] = {gate, up};
-    if (skinny_group(pair, 2, m)) {
+    if (skinny_group(pair, 2, m, forced)) {
         float* dsts[2] = {dst_dev, nullptr};
-        return run_skinny_group(pair, 2, m, k, lhs_dev, dsts, workspace_dev, workspace_bytes, true, stream);
+        return run_skinny_group(pair, 2, m, k, lhs_dev, dsts, workspace_dev, workspace_bytes, true, stream, forced);
     }
-    if (shared_quantize(pair, 2, m)) {
+    if (shared_quantize(pair, 2, m, forced)) {
         DeviceGuard g(gate->device);
         if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
-        st = xnq_quantize_lhs(gate->L.dtype, m, k, lhs_dev, workspace_dev, stream);
-        if (!st) st = xnq_qtensor_matmul_preq(gate, m, k, n, workspace_dev, off, dst_dev, stream);
-        if (!st) st = xnq_qtensor_matmul_preq(up, m, k, n, workspace_dev, off, u, stream);
+        st = quantize_lhs_impl(gate->L.dtype, m, k, lhs_dev, workspace_dev, stream, forced);
+        if (!st) st = matmul_preq_impl(gate, m, k, n, workspace_dev, off, dst_dev, stream, forced);
+        if (!st) st = matmul_preq_impl(up, m, k, n, workspace_dev, off, u, stream, forced);
     } else {
-        st = xnq_qtensor_matmul_t_ws(gate, m, k, n, lhs_dev, workspace_dev, off, dst_dev, stream);
-        if (!st) st = xnq_qtensor_matmul_t_ws(up, m, k, n, lhs_dev, workspace_dev, off, u, stream);
+        st = matmul_t_ws_impl(gate, m, k, n, lhs_dev, workspace_dev, off, dst_dev, stream, forced);
+        if (!st) st = matmul_t_ws_impl(up, m, k, n, lhs_dev, workspace_dev, off, u, stream, forced);
     }
     if (st) return st;
     DeviceGuard g(gate->device);
@@ -724,18 +773,22 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     return XNQ_OK;
 }
 
-size_t xnq_matmul_t_group_workspace_size(const xnq_qtensor* const* qts, size_t count, size_t m) {
-    if (!qts || group_route(qts, count, m)) return 0;
+static size_t group_ws_impl(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
+    if (!qts || group_route(qts, count, m, forced)) return 0;
     size_t need = 0;
     for (size_t i = 0; i < count; i++) {
-        const size_t b = qts[i] ? xnq_qtensor_matmul_t_workspace_size(qts[i], m) : 0;
+        const size_t b = qts[i] ? matmul_t_workspace_size_impl(qts[i], m, forced) : 0;
         if (b > need) need = b;
     }
-    if (count <= (size_t)kMaxGroup && skinny_group(qts, count, m)) {
-        const size_t one = skinny_group_ws(qts, count, m);
+    if (count <= (size_t)kMaxGroup && skinny_group(qts, count, m, forced)) {
+        const size_t one = skinny_group_ws(qts, count, m, forced);
         if (one > need) need = one;
     }
     return need;
+}
+
+size_t xnq_matmul_t_group_workspace_size(const xnq_qtensor* const* qts, size_t count, size_t m) {
+    return group_ws_impl(qts, count, m, g_route.load());
 }
 
 xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
@@ -751,7 +804,8 @@ xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_
     if (!lhs_dev) return fail(XNQ_ERR_INVALID, "null pointer");
     for (size_t i = 0; i < count; i++)
         if (!dsts_dev[i]) return fail(XNQ_ERR_INVALID, "null pointer");
-    if (group_route(qts, count, m)) {
+    const int forced = g_route.load();
+    if (group_route(qts, count, m, forced)) {
         const xnq_status st = check_lhs(qts[0]->L.dtype, k);
         if (st) return st;
         DeviceGuard g(qts[0]->device);
@@ -760,25 +814,26 @@ xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_
         if (e != hipSuccess) return hip_fail(e, "grouped matvec kernel");
         return XNQ_OK;
     }
-    if (count <= (size_t)kMaxGroup && skinny_group(qts, count, m))
-        return run_skinny_group(qts, count, m, k, lhs_dev, dsts_dev, workspace_dev, workspace_bytes, false, stream);
-    if (shared_quantize(qts, count, m)) {
+    if (count <= (size_t)kMaxGroup && skinny_group(qts, count, m, forced))
+        return run_skinny_group(qts, count, m, k, lhs_dev, dsts_dev, workspace_dev, workspace_bytes, false, stream,
+                                forced);
+    if (shared_quantize(qts, count, m, forced)) {
         // one activation image for every weight, then one matmul each
-        const size_t need = act_layout(qts[0]->L.dtype, m, k).bytes;
+        const size_t need = act_layout(qts[0]->L.dtype, m, k, forced).bytes;
         if (!workspace_dev || workspace_bytes < need)
             return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu the activation needs",
                         workspace_bytes, need);
         DeviceGuard g(qts[0]->device);
         if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
-        xnq_status st = xnq_quantize_lhs(qts[0]->L.dtype, m, k, lhs_dev, workspace_dev, stream);
+        xnq_status st = quantize_lhs_impl(qts[0]->L.dtype, m, k, lhs_dev, workspace_dev, stream, forced);
         for (size_t i = 0; i < count && !st; i++)
-            st = xnq_qtensor_matmul_preq(qts[i], m, k, qts[i]->L.n, workspace_dev, workspace_bytes, dsts_dev[i],
-                                         stream);
+            st = matmul_preq_impl(qts[i], m, k, qts[i]->L.n, workspace_dev, workspace_bytes, dsts_dev[i], stream,
+                                  forced);
         return st;
     }
     for (size_t i = 0; i < count; i++) {
-        const xnq_status st = xnq_qtensor_matmul_t_ws(qts[i], m, k, qts[i]->L.n, lhs_dev, workspace_dev,
-                                                      workspace_bytes, dsts_dev[i], stream);
+        const xnq_status st = matmul_t_ws_impl(qts[i], m, k, qts[i]->L.n, lhs_dev, workspace_dev, workspace_bytes,
+                                               dsts_dev[i], stream, forced);
         if (st) return st;
     }
     return XNQ_OK;
@@ -840,7 +895,7 @@ xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* w
     if (!workspace_dev || !out_dev) return fail(XNQ_ERR_INVALID, "null pointer");
     DeviceGuard g(qt->device);
     const WView w = make_wview(qt->L, qt->buf);
-    const AView a = make_aview(act_layout(qt->L.dtype, m, qt->L.k), workspace_dev);
+    const AView a = make_aview(act_layout(qt->L.dtype, m, qt->L.k, g_route.load()), workspace_dev);
     hipError_t e = launch_block_ints(w, a, m, out_dev, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "block_ints");
     return XNQ_OK;

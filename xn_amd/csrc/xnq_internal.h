@@ -154,7 +154,7 @@ struct WGroup {
 };
 
 bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string* err);
-ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k);
+ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k, int forced_route);
 uint32_t vec_dot_type(uint32_t weight_dtype);
 size_t type_size(uint32_t dtype);
 size_t block_size(uint32_t dtype);
@@ -187,6 +187,10 @@ inline AView make_aview(const ALayout& L, const void* base) {
     v.T = L.tile;
     return v;
 }
+
+// Raises a kernel's dynamic LDS limit to `bytes` on the current device, once
+// per (kernel, device); safe to call from several host threads.
+hipError_t set_max_lds(const void* kernel, int bytes);
 
 // ---------------------------------------------------------------------------
 // Launchers (each returns hipSuccess or the first HIP error).
