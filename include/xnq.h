@@ -120,6 +120,22 @@ xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, si
                                    const float* lhs_dev, void* workspace_dev, size_t workspace_bytes,
                                    float* dst_dev, void* stream);
 
+/* matmul_t that allocates nothing: no reference counterpart.  For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same contract and
+ * results as xnq_qtensor_matmul_t / xnq_qtensor_matmul_t_ws (the same
+ * kernels), with the workspace taken from a static device array of
+ * XNQ_NOALLOC_SCRATCH_BYTES per GPU that the library holds until the
+ * process ends.  Fails with XNQ_ERR_INVALID when
+ * xnq_qtensor_matmul_t_workspace_size(qt, m) exceeds it (at K = 4096 that
+ * is past about 3000 rows).  Every call on one GPU uses that GPU's one
+ * array: calls that overlap on one GPU (different streams, or host threads
+ * without ordering between them) race and must be serialised by the
+ * caller, e.g. by issuing them on one stream. */
+#define XNQ_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+xnq_status xnq_qtensor_matmul_t_noalloc(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
+                                        const float* lhs_dev, float* dst_dev, void* stream);
+
 /* Decode-step groups (no reference entry point of their own: they compute
  * what two or three QMatMul calls on one activation compute, in one launch
  * for m == 1).

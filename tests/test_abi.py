@@ -44,7 +44,7 @@ def test_sizes_match_ggml(lib):
         if lib.xnq_type_size(int(dt)):
             assert lib.xnq_type_size(int(dt)) == dt.type_size()
             assert lib.xnq_block_size(int(dt)) == dt.block_size()
-    assert lib.xnq_abi_version() == 4
+    assert lib.xnq_abi_version() == 5
 
 
 def test_host_validation(lib):

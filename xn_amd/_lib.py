@@ -38,6 +38,7 @@ SIGNATURES = {
     "xnq_qtensor_matmul_t": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_void]),
     "xnq_qtensor_matmul_t_workspace_size": (c_size, [c_void, c_size]),
     "xnq_qtensor_matmul_t_ws": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void]),
+    "xnq_qtensor_matmul_t_noalloc": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_void]),
     "xnq_matmul_t_silu_gate_workspace_size": (c_size, [c_void, c_void, c_size]),
     "xnq_matmul_t_silu_gate": (c_int, [c_void, c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void]),
     "xnq_matmul_t_group_workspace_size": (c_size, [ctypes.POINTER(c_void), c_size, c_size]),

@@ -263,7 +263,7 @@ extern "C" {
 
 const char* xnq_last_error(void) { return g_err.c_str(); }
 
-int xnq_abi_version(void) { return 4; }
+int xnq_abi_version(void) { return 5; }
 
 size_t xnq_type_size(uint32_t dtype) { return type_size(dtype); }
 size_t xnq_block_size(uint32_t dtype) { return block_size(dtype); }
@@ -611,6 +611,57 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
     st = matmul_t_ws_impl(qt, m, k, n, lhs_dev, ws, ws_bytes, dst_dev, stream, forced);
     (void)hipFreeAsync(ws, s);
     return st;
+}
+
+// ---------------------------------------------------------------------------
+// matmul_t without any allocation: the workspace is a file-scope device
+// array.  In host code `scratch` only names the symbol; its device address
+// (one per GPU) comes from hipGetSymbolAddress with that GPU current, and
+// only that address is ever handed to kernels.
+
+static __device__ __align__(256) uint8_t scratch[XNQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// Device address of `scratch` on `dev`, which must be the current device.
+static xnq_status scratch_ptr(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxDevices) return fail(XNQ_ERR_INVALID, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(XNQ_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return XNQ_OK;
+}
+
+xnq_status xnq_qtensor_matmul_t_noalloc(const xnq_qtensor* qt, size_t m, size_t k, size_t n, const float* lhs_dev,
+                                        float* dst_dev, void* stream) {
+    xnq_status st = check_mkn(qt, m, k, n);
+    if (st) return st;
+    const int forced = g_route.load();
+    const size_t need = matmul_t_workspace_size_impl(qt, m, forced);
+    if (need > XNQ_NOALLOC_SCRATCH_BYTES)
+        return fail(XNQ_ERR_INVALID,
+                    "matmul_t_noalloc: m = %zu needs %zu bytes of scratch, more than the library's static %zu; "
+                    "split the rows or use matmul_t_ws",
+                    m, need, (size_t)XNQ_NOALLOC_SCRATCH_BYTES);
+    if (need == 0 || m == 0 || n == 0) return matmul_t_ws_impl(qt, m, k, n, lhs_dev, nullptr, 0, dst_dev, stream, forced);
+    DeviceGuard g(qt->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    void* ws = nullptr;
+    st = scratch_ptr(qt->device, &ws);
+    if (st) return st;
+    // every kernel writes the scratch it reads (activation image, split-K
+    // partials) before reading it, so nothing needs clearing between calls
+    return matmul_t_ws_impl(qt, m, k, n, lhs_dev, ws, XNQ_NOALLOC_SCRATCH_BYTES, dst_dev, stream, forced);
 }
 
 // ---------------------------------------------------------------------------

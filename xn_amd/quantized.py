@@ -293,6 +293,14 @@ class QTensor:
                                                   _ptr(ws) if ws is not None else None, nbytes, _ptr(dst),
                                                   _stream(self.device)))
 
+    def matmul_t_noalloc(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
+        """matmul_t with the library's static per-GPU scratch
+        (xnq_qtensor_matmul_t_noalloc): allocates nothing; calls on one GPU
+        must not overlap."""
+        m, k, n = self._check_mm(mkn, lhs, dst)
+        check(_lib.load().xnq_qtensor_matmul_t_noalloc(self.storage.handle, m, k, n, _ptr(lhs), _ptr(dst),
+                                                       _stream(self.device)))
+
     def matmul_t_split(self, mkn: Tuple[int, int, int], lhs: torch.Tensor, dst: torch.Tensor) -> None:
         """quantize_lhs then matmul_preq as two library calls, for every m
         (k_quants.rs:2014-2026: quantize_lhs, then T::matmul)."""
