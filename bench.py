@@ -43,8 +43,9 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=512)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "sweep", "decode"], default="all",
+    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "stream", "sweep", "decode"], default="all",
                    help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters); "
+                        "'stream' times a bare read of the headline weight's bytes (the matvec's ceiling); "
                         "'sweep' times every configured shape (matvec sweep, FFN, prefill, decode step)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one instead of replaying a HIP graph (for counter runs)")
@@ -237,43 +238,50 @@ def sweep(args, dev, stream, gen) -> dict:
         del ws
 
     # config 5: every QMatMul of one decode step (random weights; attention itself is out of scope)
+    from xn_amd.decode import DecoderWeights, DecodeStep
+
     d, kv, ff, vocab, layers = 4096, 1024, 14336, 128256, 32
-    mats, layer_w = [], []
-    for _ in range(layers):
-        lw = [make(12, d, d), make(12, kv, d), make(12, kv, d), make(12, d, d), make(12, ff, d), make(12, ff, d),
-              make(14, d, ff)]
-        layer_w.append(lw)
-        mats += [(lw[0], d, d), (lw[1], d, kv), (lw[2], d, kv), (lw[3], d, d), (lw[4], d, ff), (lw[5], d, ff),
-                 (lw[6], ff, d)]
-    head = make(14, vocab, d)
-    mats.append((head, d, vocab))
-    wtotal = sum(qbytes(12 if q.dtype() == GgmlDType.Q4K else 14, n, kk) for q, kk, n in mats)
+    dw = DecoderWeights.random(layers, d, kv, ff, vocab, dev, generator=gen)
+    mats = [(q, q.shape()[1], q.shape()[0]) for lw in dw.layers for q in lw.all()] + \
+           [(dw.lm_head, d, vocab)]
+    wtotal = dw.weight_bytes()
     for b in (1, 16):
         xs = {kk: torch.randn((b, kk), generator=gen, device=dev) for kk in (d, ff)}
         ys = {n: torch.empty((b, n), device=dev) for n in (d, kv, ff, vocab)}
-        yk = torch.empty((b, kv), device=dev)
 
         def step(i):
             for q, kk, n in mats:
                 q.matmul_t((b, kk, n), xs[kk], ys[n])
 
-        def step_grouped(i):
-            # q, k, v in one launch; gate and up with the SiLU gate in one launch
-            for lw in layer_w:
-                matmul_t_group(lw[0:3], b, d, xs[d], [ys[d], ys[kv], yk])
-                lw[3].matmul_t((b, d, d), xs[d], ys[d])
-                matmul_t_silu_gate(lw[4], lw[5], (b, d, ff), xs[d], ys[ff])
-                lw[6].matmul_t((b, ff, d), xs[ff], ys[d])
-            head.matmul_t((b, d, vocab), xs[d], ys[vocab])
-
-        for name, fn in (("5 decode step (225 QMatMuls, one call each)", step),
-                         ("5 decode step (q/k/v grouped, SiLU-gated gate/up)", step_grouped)):
-            ms = timed(fn, 3)
-            rows.append({"config": name, "batch": b, "weight_bytes": wtotal,
-                         "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
-                         "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
-            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
-    del mats, layer_w
+        ms = timed(step, 3)
+        rows.append({"config": "5 decode step (225 QMatMuls, one call each)", "batch": b, "weight_bytes": wtotal,
+                     "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        # the product driver: q/k/v grouped, SiLU-gated gate/up, one captured graph per step
+        ds = DecodeStep(dw, b, dev)
+        ds.x.normal_(generator=gen)
+        ds.capture(stream)
+        for _ in range(3):
+            ds.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(5):
+                ds.replay()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) / 5)
+        ms = float(np.median(times))
+        rows.append({"config": "5 decode step (DecodeStep: q/k/v grouped, SiLU-gated gate/up, one graph)",
+                     "batch": b, "weight_bytes": wtotal,
+                     "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del ds
+    del mats, dw
     return {"metric": "per-config sweep", "rows": rows}
 
 
@@ -321,6 +329,24 @@ def main():
         print(json.dumps({"metric": "device copy GB/s (read + write)", "bytes_read": nbytes,
                           "bytes_written": nbytes, "ms_per_copy": round(ms, 5),
                           "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}), flush=True)
+        return
+
+    if args.only == "stream":
+        from xn_amd.quantized import stream_read
+
+        nbytes = weight_bytes(N_DIM, K_DIM)
+        ncopy = max(2, (600 << 20) // nbytes + 1)  # past the 256 MB Infinity Cache
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(i + 1) for i in range(ncopy)]
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                stream_read(bufs[i % ncopy], sink)
+            g = capture(lambda i: stream_read(bufs[i % ncopy], sink), args.steps, stream, args.eager)
+        ms = time_graph(g, stream) / args.steps
+        print(json.dumps({"metric": "bare HBM read GB/s of the 4096x14336 Q4_K weight bytes",
+                          "bytes_per_launch": nbytes, "copies": ncopy, "us_per_read": round(ms * 1e3, 3),
+                          "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                          "frac_of_8TBs": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
         return
 
     if args.only in ("sweep", "decode"):

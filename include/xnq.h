@@ -219,6 +219,14 @@ xnq_status xnq_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const
 xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* workspace_dev,
                                   int32_t* out_dev, void* stream);
 
+/* Measurement hook, no counterpart in the reference: reads `bytes` (a
+ * multiple of 16) of device memory at `src_dev` with the matvec kernels'
+ * access pattern (dwordx4, non-temporal, 4 loads in flight per lane, a grid
+ * of 4-wavefront workgroups filling the GPU) and XORs every 32-bit word into
+ * *sink_dev (which the caller zeroes).  Its time is the ceiling a weight
+ * stream of that size reaches on this GPU. */
+xnq_status xnq_stream_read(const void* src_dev, size_t bytes, uint32_t* sink_dev, void* stream);
+
 /* Stream capture into a replayable graph (xn's Device::capture_begin /
  * capture_end / CaptureGraph::launch, cuda_backend/mod.rs:251-283): every
  * launch the library makes on `stream` between begin and end is recorded,

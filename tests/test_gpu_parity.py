@@ -387,3 +387,18 @@ def test_matmul_t_refuses_to_allocate_in_capture(orc, dev):
             st = _lib.load().xnq_qtensor_matmul_t(qt.storage.handle, 300, k, n, x.data_ptr(), y.data_ptr(),
                                                   stream.cuda_stream)
             _lib.check(st)
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096, 1 << 20, (3 << 20) + 48])
+def test_stream_read_folds_every_word(dev, nbytes):
+    """The bare-read measurement hook reads every 32-bit word: its XOR fold
+    equals numpy's, including a ragged tail past the last full round."""
+    from xn_amd.quantized import stream_read
+
+    host = np.random.default_rng(nbytes).integers(0, 2**32, nbytes // 4, dtype=np.uint32)
+    buf = torch.from_numpy(host.view(np.uint8).copy()).to(dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream_read(buf, sink)
+    torch.cuda.synchronize()
+    want = np.bitwise_xor.reduce(host)
+    assert int(sink.cpu().numpy().view(np.uint32)[0]) == int(want)

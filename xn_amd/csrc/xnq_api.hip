@@ -961,6 +961,14 @@ struct xnq_graph {
     hipGraphExec_t exec = nullptr;
 };
 
+xnq_status xnq_stream_read(const void* src_dev, size_t bytes, uint32_t* sink_dev, void* stream) {
+    if (bytes % 16) return fail(XNQ_ERR_INVALID, "stream_read: %zu bytes is not a multiple of 16", bytes);
+    if (bytes && (!src_dev || !sink_dev)) return fail(XNQ_ERR_INVALID, "null pointer");
+    const hipError_t e = launch_stream_read(src_dev, bytes, sink_dev, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "stream_read kernel");
+    return XNQ_OK;
+}
+
 xnq_status xnq_capture_begin(void* stream) {
     if (!stream) return fail(XNQ_ERR_INVALID, "stream capture needs a stream other than the null stream");
     const hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeRelaxed);

@@ -491,6 +491,14 @@ class capture:
 
 # -- lower-level entry points used by tests and the benchmark ------------------
 
+def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    """Bare read of `buf`'s bytes folded by XOR into the int32 `sink`
+    (xnq_stream_read): the weight-stream ceiling, for measurement."""
+    if not buf.is_cuda or not buf.is_contiguous() or sink.dtype != torch.int32 or not sink.is_cuda:
+        raise XnqError(1, "stream_read: contiguous device buffer and an int32 device sink")
+    check(_lib.load().xnq_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream(buf.device)))
+
+
 def set_route(route: int) -> None:
     """0 = route by m, 1 = force the matvec kernel, 2 = force the MFMA kernel."""
     check(_lib.load().xnq_set_route(int(route)))
