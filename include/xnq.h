@@ -80,7 +80,8 @@ xnq_status xnq_qtensor_upload_device(int device, uint32_t dtype, const void* ggu
 
 /* Quantize an n x k f32 weight that lives in device memory.  Replaces
  * QTensor::quantize_f32 (mod.rs:283-303), i.e. the per-dtype
- * GgmlType::from_float (k_quants.rs:235-270, 636-661, 1418-1473, 1801-1871);
+ * GgmlType::from_float (k_quants.rs:235-270, 345-377, 442-476, 546-583, 636-661,
+ * 951-1011, 1170-1236, 1418-1473, 1608-1679, 1801-1871) for every device dtype;
  * the blocks produced are byte-identical to the CPU quantizer's. */
 xnq_status xnq_qtensor_quantize(int device, uint32_t dtype, const float* src_dev, size_t n,
                                 size_t k, void* stream, xnq_qtensor** out);

@@ -100,13 +100,27 @@ def test_odd_block_count_rejected(orc, dev, dt):
         qt.matmul_t((1, k, n), x, dst)
 
 
-def test_device_quantizer_refuses(dev):
+@pytest.mark.parametrize("dt", MORE)
+def test_device_weight_quantizer_bit_exact(orc, dev, dt):
+    """QTensor::quantize_f32 on the device (mod.rs:283-303) writes the bytes
+    xn's from_float does (k_quants.rs:345-377, 442-476, 546-583, 951-1011,
+    1170-1236, 1608-1679): N(0, 0.02) rows plus a zero row, a constant row,
+    an all-positive row (min clamps to 0), a ramp, single outliers and
+    magnitudes near the f16 subnormal range."""
     from xn_amd import GgmlDType, QTensor
-    from xn_amd._lib import XnqError
 
-    w = torch.zeros((4, 256), dtype=torch.float32, device=dev)
-    with pytest.raises(XnqError, match="no device quantizer"):
-        QTensor.quantize_f32(w, (4, 256), GgmlDType.Q5K)
+    rng = np.random.default_rng(4100 + dt)
+    n, k = 24, 2048
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    w[1] = 0.0
+    w[2] = 0.125
+    w[3, :256] = np.linspace(-1, 1, 256, dtype=np.float32)
+    w[4] = np.abs(w[4]) + 0.01
+    w[5, ::37] = 0.75
+    w[6] *= 1e-4
+    w[7, 5] = -0.9
+    qt = QTensor.quantize_f32(torch.from_numpy(w).to(dev), (n, k), GgmlDType(dt))
+    assert qt.data() == orc.from_float(dt, w).tobytes()
 
 
 @pytest.mark.parametrize("dt", [Q4_1, Q5K])

@@ -1,7 +1,7 @@
 // Quantizers on the device, bit-identical to xn's CPU quantizers:
 //   * activations ("lhs") to Q8_0 / Q8_K, into the private planar workspace
 //     used by the matmul kernels or into canonical GGUF blocks;
-//   * weights (QTensor::quantize_f32) to Q8_0 / Q4_0 / Q4_K / Q6_K GGUF blocks.
+//   * weights (QTensor::quantize_f32) to GGUF blocks of every device dtype.
 // No multiply-add is fused in this file, so every f32 operation rounds exactly
 // where the reference's does.
 #pragma clang fp contract(off)
@@ -142,12 +142,13 @@ __device__ __forceinline__ int32_t total_key(float f) {
     return i ^ (int32_t)(((uint32_t)(i >> 31)) >> 1);
 }
 
-// utils.rs:205-254 make_qkx1_quants(nmax, ntry, x[0..32]); returns scale, -min.
-__device__ float make_qkx1_quants32(int nmax, int ntry, const float* x, float* neg_min) {
-    uint8_t l[32];
-    for (int i = 0; i < 32; i++) l[i] = 0;
+// utils.rs:205-254 make_qkx1_quants(nmax, ntry, x[0..N]); returns scale, -min.
+template <int N>
+__device__ float make_qkx1_quants(int nmax, int ntry, const float* x, float* neg_min) {
+    uint8_t l[N];
+    for (int i = 0; i < N; i++) l[i] = 0;
     float mn = x[0], mx = x[0];
-    for (int i = 1; i < 32; i++) {
+    for (int i = 1; i < N; i++) {
         if (total_key(x[i]) < total_key(mn)) mn = x[i];
         if (total_key(x[i]) >= total_key(mx)) mx = x[i];
     }
@@ -162,7 +163,7 @@ __device__ float make_qkx1_quants32(int nmax, int ntry, const float* x, float* n
         float sumlx = 0.0f;
         int32_t suml2 = 0;
         bool did_change = false;
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < N; i++) {
             const float value = x[i];
             const int32_t li = clampi(nearest_int(iscale * (value - min)), 0, nmax);
             const uint8_t cl = (uint8_t)li;
@@ -175,8 +176,8 @@ __device__ float make_qkx1_quants32(int nmax, int ntry, const float* x, float* n
         }
         scale = sumlx / (float)suml2;
         float sum = -0.0f;
-        for (int i = 0; i < 32; i++) sum += x[i] - scale * (float)l[i];
-        min = sum / 32.0f;
+        for (int i = 0; i < N; i++) sum += x[i] - scale * (float)l[i];
+        min = sum / (float)N;
         if (min > 0.0f) min = 0.0f;
         iscale = 1.0f / scale;
         if (!did_change) break;
@@ -203,7 +204,7 @@ __global__ void w_q4k_kernel(const float* __restrict__ xin, size_t nblocks, uint
     uint8_t sc12[12];
     for (int i = 0; i < 12; i++) sc12[i] = 0;
     float mins[8], scales[8];
-    for (int j = 0; j < 8; j++) scales[j] = make_qkx1_quants32(15, 5, x + 32 * j, &mins[j]);
+    for (int j = 0; j < 8; j++) scales[j] = make_qkx1_quants<32>(15, 5, x + 32 * j, &mins[j]);
     float max_scale = 0.0f, max_min = 0.0f;
     for (int j = 0; j < 8; j++) {
         max_scale = fmaxf(scales[j], max_scale);
@@ -384,6 +385,305 @@ __global__ void w_q6k_kernel(const float* __restrict__ xin, size_t nblocks, uint
     }
 }
 
+// ---------------------------------------------------------------------------
+// The other GGUF weight types, one thread per block, step for step as xn's
+// from_float.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void put16(uint8_t* p, uint16_t v) {
+    p[0] = (uint8_t)v;
+    p[1] = (uint8_t)(v >> 8);
+}
+__device__ __forceinline__ void put32(uint8_t* p, uint32_t v) {
+    for (int i = 0; i < 4; i++) p[i] = (uint8_t)(v >> (8 * i));
+}
+
+// k_quants.rs:345-377 BlockQ4_1::from_float: {d, m, qs[16]}
+__global__ void w_q41_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float* x = xin + i * 32;
+    uint8_t* b = out + i * 20;
+    float min = INFINITY, max = -INFINITY;
+    for (int j = 0; j < 32; j++) {
+        min = fminf(x[j], min);
+        max = fmaxf(x[j], max);
+    }
+    const float d = (max - min) / 15.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    put16(b, f32_to_f16_bits(d));
+    put16(b + 2, f32_to_f16_bits(min));
+    for (int j = 0; j < 16; j++) {
+        uint8_t xi0 = f_as_u8((x[j] - min) * id + 0.5f), xi1 = f_as_u8((x[16 + j] - min) * id + 0.5f);
+        if (xi0 > 15) xi0 = 15;
+        if (xi1 > 15) xi1 = 15;
+        b[4 + j] = (uint8_t)(xi0 | (xi1 << 4));
+    }
+}
+
+// k_quants.rs:442-476 BlockQ5_0::from_float: {d, qh[4], qs[16]}
+__global__ void w_q50_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float* x = xin + i * 32;
+    uint8_t* b = out + i * 22;
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < 32; j++)
+        if (amax < fabsf(x[j])) {
+            amax = fabsf(x[j]);
+            max = x[j];
+        }
+    const float d = max / -16.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    put16(b, f32_to_f16_bits(d));
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; j++) {
+        const int8_t a0 = f_as_i8(x[j] * id + 16.5f), a1 = f_as_i8(x[j + 16] * id + 16.5f);
+        const uint8_t xi0 = (uint8_t)(a0 < 31 ? a0 : 31), xi1 = (uint8_t)(a1 < 31 ? a1 : 31);
+        b[6 + j] = (uint8_t)((xi0 & 0x0F) | ((xi1 & 0x0F) << 4));
+        qh |= (((uint32_t)xi0 & 0x10) >> 4) << j;
+        qh |= (((uint32_t)xi1 & 0x10) >> 4) << (j + 16);
+    }
+    put32(b + 2, qh);
+}
+
+// k_quants.rs:546-583 BlockQ5_1::from_float: {d, m, qh[4], qs[16]}
+__global__ void w_q51_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float* x = xin + i * 32;
+    uint8_t* b = out + i * 24;
+    float min = INFINITY, max = -INFINITY;
+    for (int j = 0; j < 32; j++) {
+        min = fminf(x[j], min);
+        max = fmaxf(x[j], max);
+    }
+    const float d = (max - min) / 31.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    put16(b, f32_to_f16_bits(d));
+    put16(b + 2, f32_to_f16_bits(min));
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; j++) {
+        const uint8_t xi0 = f_as_u8((x[j] - min) * id + 0.5f), xi1 = f_as_u8((x[16 + j] - min) * id + 0.5f);
+        b[8 + j] = (uint8_t)((xi0 & 0x0F) | ((xi1 & 0x0F) << 4));
+        qh |= (((uint32_t)xi0 & 0x10) >> 4) << j;
+        qh |= (((uint32_t)xi1 & 0x10) >> 4) << (j + 16);
+    }
+    put32(b + 4, qh);
+}
+
+// k_quants.rs:951-1011 BlockQ2K::from_float: {scales[16], qs[64], d, dmin}
+__global__ void w_q2k_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t bi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (bi >= nblocks) return;
+    const float* x = xin + bi * 256;
+    uint8_t* b = out + bi * 84;
+    uint8_t* sc = b;
+    const float q4scale = 15.0f;
+    float mins[16], scales[16];
+    for (int j = 0; j < 16; j++) scales[j] = make_qkx1_quants<16>(3, 5, x + 16 * j, &mins[j]);
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 16; j++) max_scale = fmaxf(scales[j], max_scale);
+    for (int j = 0; j < 16; j++) max_min = fmaxf(mins[j], max_min);
+    uint16_t dh, mh;
+    if (max_scale > 0.0f) {
+        const float iscale = q4scale / max_scale;
+        for (int j = 0; j < 16; j++) sc[j] = (uint8_t)nearest_int(iscale * scales[j]);
+        dh = f32_to_f16_bits(max_scale / q4scale);
+    } else {
+        for (int j = 0; j < 16; j++) sc[j] = 0;
+        dh = f32_to_f16_bits(0.0f);
+    }
+    if (max_min > 0.0f) {
+        const float iscale = q4scale / max_min;
+        for (int j = 0; j < 16; j++) sc[j] = (uint8_t)(sc[j] | (uint8_t)((uint8_t)nearest_int(iscale * mins[j]) << 4));
+        mh = f32_to_f16_bits(max_min / q4scale);
+    } else {
+        mh = f32_to_f16_bits(0.0f);
+    }
+    put16(b + 80, dh);
+    put16(b + 82, mh);
+    uint8_t L[256];
+    for (int e = 0; e < 256; e++) L[e] = 0;
+    const float df = f16_bits_to_f32(dh), mf = f16_bits_to_f32(mh);
+    for (int j = 0; j < 16; j++) {
+        const float d = df * (float)(sc[j] & 0xF);
+        if (d == 0.0f) continue;
+        const float dm = mf * (float)(sc[j] >> 4);
+        for (int ii = 0; ii < 16; ii++) L[16 * j + ii] = (uint8_t)clampi(nearest_int((x[16 * j + ii] + dm) / d), 0, 3);
+    }
+    for (int j = 0; j < 256; j += 128)
+        for (int l = 0; l < 32; l++)
+            b[16 + j / 4 + l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 2) | (L[j + l + 64] << 4) | (L[j + l + 96] << 6));
+}
+
+// utils.rs:257-320 make_q3_quants(x[0..16], nmax, do_rmse = true): scale of levels -nmax..nmax-1
+__device__ float make_q3_quants16(int nmax, const float* x) {
+    int8_t l[16];
+    float max = 0.0f, amax = 0.0f;
+    for (int i = 0; i < 16; i++) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
+        }
+    }
+    if (amax == 0.0f) return 0.0f;
+    const float iscale = -(float)nmax / max;
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < 16; i++) {
+        const int32_t li = clampi(f_as_i32(roundf(iscale * x[i])), -nmax, nmax - 1);
+        l[i] = (int8_t)li;
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * (float)li;
+        suml2 += w * (float)(li * li);
+    }
+    for (int it = 0; it < 5; it++) {
+        int n_changed = 0;
+        for (int i = 0; i < 16; i++) {
+            const float w = x[i] * x[i];
+            float slx = sumlx - w * x[i] * (float)l[i];
+            if (slx > 0.0f) {
+                float sl2 = suml2 - w * (float)((int32_t)l[i] * (int32_t)l[i]);
+                const int32_t new_l = clampi(f_as_i32(roundf(x[i] * sl2 / slx)), -nmax, nmax - 1);
+                if (new_l != (int32_t)l[i]) {
+                    slx += w * x[i] * (float)new_l;
+                    sl2 += w * (float)(new_l * new_l);
+                    if (sl2 > 0.0f && slx * slx * suml2 > sumlx * sumlx * sl2) {
+                        l[i] = (int8_t)new_l;
+                        sumlx = slx;
+                        suml2 = sl2;
+                        n_changed++;
+                    }
+                }
+            }
+        }
+        if (n_changed == 0) break;
+    }
+    return sumlx / suml2;
+}
+
+// k_quants.rs:1170-1236 BlockQ3K::from_float: {hmask[32], qs[64], scales[12], d}
+__global__ void w_q3k_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t bi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (bi >= nblocks) return;
+    const float* x = xin + bi * 256;
+    uint8_t* b = out + bi * 110;
+    uint8_t* hmask = b;
+    uint8_t* qs = b + 32;
+    uint8_t* sc = b + 96;
+    float scales[16];
+    for (int j = 0; j < 16; j++) scales[j] = make_q3_quants16(4, x + 16 * j);
+    float max_scale = 0.0f;
+    for (int j = 0; j < 16; j++)
+        if (fabsf(scales[j]) > fabsf(max_scale)) max_scale = scales[j];
+    for (int j = 0; j < 12; j++) sc[j] = 0;
+    uint16_t dh;
+    if (max_scale != 0.0f) {
+        const float iscale = -32.0f / max_scale;
+        for (int j = 0; j < 16; j++) {
+            int32_t l = clampi(nearest_int(iscale * scales[j]), -32, 31) + 32;
+            if (j < 8) sc[j] = (uint8_t)(l & 0xF);
+            else sc[j - 8] = (uint8_t)(sc[j - 8] | (uint8_t)((l & 0xF) << 4));
+            l >>= 4;
+            sc[j % 4 + 8] = (uint8_t)(sc[j % 4 + 8] | (uint8_t)(l << (2 * (j / 4))));
+        }
+        dh = f32_to_f16_bits(1.0f / iscale);
+    } else {
+        dh = f32_to_f16_bits(0.0f);
+    }
+    put16(b + 108, dh);
+    int8_t L[256];
+    for (int e = 0; e < 256; e++) L[e] = 0;
+    const float df = f16_bits_to_f32(dh);
+    for (int j = 0; j < 16; j++) {
+        const uint8_t s4 = j < 8 ? (uint8_t)(sc[j] & 0xF) : (uint8_t)(sc[j - 8] >> 4);
+        const int8_t sci = (int8_t)((int8_t)(uint8_t)(s4 | (((sc[8 + j % 4] >> (2 * (j / 4))) & 3) << 4)) - 32);
+        const float d = df * (float)sci;
+        if (d != 0.0f)
+            for (int ii = 0; ii < 16; ii++) L[16 * j + ii] = (int8_t)(clampi(nearest_int(x[16 * j + ii] / d), -4, 3) + 4);
+    }
+    for (int j = 0; j < 32; j++) hmask[j] = 0;
+    int m = 0;
+    uint8_t hm = 1;
+    for (int e = 0; e < 256; e++) {
+        if (L[e] > 3) {
+            hmask[m] |= hm;
+            L[e] = (int8_t)(L[e] - 4);
+        }
+        if (++m == 32) {
+            m = 0;
+            hm = (uint8_t)(hm << 1);
+        }
+    }
+    for (int j = 0; j < 256; j += 128)
+        for (int l = 0; l < 32; l++)
+            qs[j / 4 + l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 2) | (L[j + l + 64] << 4) | (L[j + l + 96] << 6));
+}
+
+// k_quants.rs:1608-1679 BlockQ5K::from_float: {d, dmin, scales[12], qh[32], qs[128]}
+__global__ void w_q5k_kernel(const float* __restrict__ xin, size_t nblocks, uint8_t* __restrict__ out) {
+    const size_t bi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (bi >= nblocks) return;
+    const float* x = xin + bi * 256;
+    uint8_t* b = out + bi * 176;
+    uint8_t* sc = b + 4;
+    uint8_t* qh = b + 16;
+    uint8_t* qs = b + 48;
+    float mins[8], scales[8];
+    for (int j = 0; j < 8; j++) scales[j] = make_qkx1_quants<32>(31, 5, x + 32 * j, &mins[j]);
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) max_scale = fmaxf(scales[j], max_scale);
+    for (int j = 0; j < 8; j++) max_min = fmaxf(mins[j], max_min);
+    const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    for (int j = 0; j < 12; j++) sc[j] = 0;
+    for (int j = 0; j < 8; j++) {
+        const int32_t ls0 = nearest_int(inv_scale * scales[j]), lm0 = nearest_int(inv_min * mins[j]);
+        const uint8_t ls = (uint8_t)(ls0 < 63 ? ls0 : 63), lm = (uint8_t)(lm0 < 63 ? lm0 : 63);
+        if (j < 4) {
+            sc[j] = ls;
+            sc[j + 4] = lm;
+        } else {
+            sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            sc[j - 4] = (uint8_t)(sc[j - 4] | ((ls >> 4) << 6));
+            sc[j] = (uint8_t)(sc[j] | ((lm >> 4) << 6));
+        }
+    }
+    const uint16_t dh = f32_to_f16_bits(max_scale / 63.0f), mh = f32_to_f16_bits(max_min / 63.0f);
+    put16(b, dh);
+    put16(b + 2, mh);
+    uint8_t L[256];
+    for (int e = 0; e < 256; e++) L[e] = 0;
+    const float df = f16_bits_to_f32(dh), mf = f16_bits_to_f32(mh);
+    for (int j = 0; j < 8; j++) {
+        uint8_t s, m;
+        get_scale_min_k4(j, sc, &s, &m);
+        const float d = df * (float)s;
+        if (d == 0.0f) continue;
+        const float dm = mf * (float)m;
+        for (int ii = 0; ii < 32; ii++) L[32 * j + ii] = (uint8_t)clampi(nearest_int((x[32 * j + ii] + dm) / d), 0, 31);
+    }
+    for (int j = 0; j < 32; j++) qh[j] = 0;
+    uint8_t m1 = 1, m2 = 2;
+    for (int nn = 0; nn < 256; nn += 64) {
+        const int off = (nn / 64) * 32;
+        for (int j = 0; j < 32; j++) {
+            uint8_t l1 = L[nn + j], l2 = L[nn + j + 32];
+            if (l1 > 15) {
+                l1 = (uint8_t)(l1 - 16);
+                qh[j] |= m1;
+            }
+            if (l2 > 15) {
+                l2 = (uint8_t)(l2 - 16);
+                qh[j] |= m2;
+            }
+            qs[off + j] = (uint8_t)(l1 | (l2 << 4));
+        }
+        m1 = (uint8_t)(m1 << 2);
+        m2 = (uint8_t)(m2 << 2);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_quantize_act(const ALayout& L, const float* x, void* ws, hipStream_t s) {
@@ -426,6 +726,12 @@ hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float*
     case XNQ_Q4_0: w_q40_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
     case XNQ_Q4K: w_q4k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
     case XNQ_Q6K: w_q6k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q4_1: w_q41_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q5_0: w_q50_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q5_1: w_q51_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q2K: w_q2k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q3K: w_q3k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
+    case XNQ_Q5K: w_q5k_kernel<<<grid, threads, 0, s>>>(x, nblocks, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

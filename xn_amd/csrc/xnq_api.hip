@@ -330,10 +330,6 @@ xnq_status xnq_qtensor_quantize(int device, uint32_t dtype, const float* src_dev
     *out = nullptr;
     xnq_status st = check_weight(dtype, n, k);
     if (st) return st;
-    if (is_raw_layout(dtype))
-        return fail(XNQ_ERR_UNSUPPORTED,
-                    "%s: no device quantizer; quantize on the host (GgmlType::from_float) and upload the blocks",
-                    dtype_name(dtype));
     if (!src_dev && n) return fail(XNQ_ERR_INVALID, "null source pointer");
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
