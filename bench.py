@@ -43,9 +43,11 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=512)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "stream", "sweep", "decode"], default="all",
+    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "stream", "probes", "sweep", "decode"],
+                   default="all",
                    help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters); "
                         "'stream' times a bare read of the headline weight's bytes (the matvec's ceiling); "
+                        "'probes' measures the matrix-core / VALU issue sharing and the LDS read bandwidth; "
                         "'sweep' times every configured shape (matvec sweep, FFN, prefill, decode step)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one instead of replaying a HIP graph (for counter runs)")
@@ -285,6 +287,50 @@ def sweep(args, dev, stream, gen) -> dict:
     return {"metric": "per-config sweep", "rows": rows}
 
 
+CLOCK_GHZ = 2.4  # MI355X peak engine clock, used to turn times into cycles
+
+
+def probes(dev, stream) -> dict:
+    """Hardware ceilings behind the kernels' designs (measurement hooks in the
+    library): int8 MFMA with independent VALU work in the same wavefront
+    ("same") or in the other wavefront of each SIMD ("split"), and the LDS
+    read bandwidth.  One workgroup of 8 wavefronts per CU."""
+    import torch
+
+    from xn_amd.quantized import probe_lds_read, probe_mfma_valu
+
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    iters = 4096
+
+    def timed(fn, reps=3):
+        with torch.cuda.stream(stream):
+            fn()
+            ts = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                fn()
+                e1.record(stream)
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+        return float(np.median(ts))
+
+    out = {"metric": "probes", "clock_ghz_assumed": CLOCK_GHZ, "mfma_valu": []}
+    for split in (False, True):
+        for rounds in (0, 2, 4, 8, 16):
+            ms = timed(lambda: probe_mfma_valu(rounds, split, iters, ncu, sink))
+            cyc = ms * 1e-3 * CLOCK_GHZ * 1e9 / iters
+            out["mfma_valu"].append({
+                "layout": "split" if split else "same", "valu_ops_per_wave_iter": 8 * rounds,
+                "mfma_per_simd_iter": 4 if split else 8, "cycles_per_iter": round(cyc, 1)})
+    ms = timed(lambda: probe_lds_read(iters, ncu, sink))
+    nbytes = ncu * 8 * 8 * 1024 * iters
+    out["lds_read"] = {"bytes_per_clk_per_cu": round(nbytes / ncu / (ms * 1e-3) / (CLOCK_GHZ * 1e9), 1),
+                       "chip_tb_s": round(nbytes / (ms * 1e-3) / 1e12, 1)}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -347,6 +393,10 @@ def main():
                           "bytes_per_launch": nbytes, "copies": ncopy, "us_per_read": round(ms * 1e3, 3),
                           "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                           "frac_of_8TBs": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+        return
+
+    if args.only == "probes":
+        print(json.dumps(probes(dev, stream)), flush=True)
         return
 
     if args.only in ("sweep", "decode"):

@@ -228,6 +228,21 @@ xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* w
  * stream of that size reaches on this GPU. */
 xnq_status xnq_stream_read(const void* src_dev, size_t bytes, uint32_t* sink_dev, void* stream);
 
+/* Measurement hooks, no counterpart in the reference: the ceilings the
+ * matmul kernels are measured against.
+ *   xnq_probe_mfma_valu: workgroups of 8 wavefronts (2 per SIMD) loop
+ *     `iters` times over 4 independent v_mfma_i32_32x32x32_i8 and
+ *     8 * valu_rounds independent integer VALU ops (valu_rounds in
+ *     0, 2, 4, 8, 16); split != 0 puts the MFMAs in wavefronts 0-3 and the
+ *     VALU work in 4-7 (one of each per SIMD).  Timing it shows whether VALU
+ *     time hides under the matrix cores.
+ *   xnq_probe_lds_read: workgroups of 8 wavefronts each read 8 conflict-free
+ *     ds_read_b128 per iteration (1 KiB per instruction).
+ * Results only keep the work live; *sink_dev is not meaningful. */
+xnq_status xnq_probe_mfma_valu(int valu_rounds, int split, int iters, int workgroups, uint32_t* sink_dev,
+                               void* stream);
+xnq_status xnq_probe_lds_read(int iters, int workgroups, uint32_t* sink_dev, void* stream);
+
 /* Stream capture into a replayable graph (xn's Device::capture_begin /
  * capture_end / CaptureGraph::launch, cuda_backend/mod.rs:251-283): every
  * launch the library makes on `stream` between begin and end is recorded,

@@ -965,6 +965,22 @@ xnq_status xnq_stream_read(const void* src_dev, size_t bytes, uint32_t* sink_dev
     return XNQ_OK;
 }
 
+xnq_status xnq_probe_mfma_valu(int valu_rounds, int split, int iters, int workgroups, uint32_t* sink_dev,
+                               void* stream) {
+    if (iters < 1 || workgroups < 1 || !sink_dev) return fail(XNQ_ERR_INVALID, "probe: bad arguments");
+    const hipError_t e = launch_probe_mfma_valu(valu_rounds, split != 0, iters, workgroups, sink_dev, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return fail(XNQ_ERR_INVALID, "probe: valu_rounds must be 0, 2, 4, 8 or 16");
+    if (e != hipSuccess) return hip_fail(e, "probe kernel");
+    return XNQ_OK;
+}
+
+xnq_status xnq_probe_lds_read(int iters, int workgroups, uint32_t* sink_dev, void* stream) {
+    if (iters < 1 || workgroups < 1 || !sink_dev) return fail(XNQ_ERR_INVALID, "probe: bad arguments");
+    const hipError_t e = launch_probe_lds_read(iters, workgroups, sink_dev, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "probe kernel");
+    return XNQ_OK;
+}
+
 xnq_status xnq_capture_begin(void* stream) {
     if (!stream) return fail(XNQ_ERR_INVALID, "stream capture needs a stream other than the null stream");
     const hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeRelaxed);

@@ -499,6 +499,17 @@ def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
     check(_lib.load().xnq_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream(buf.device)))
 
 
+def probe_mfma_valu(valu_rounds: int, split: bool, iters: int, workgroups: int, sink: torch.Tensor) -> None:
+    """Measurement hook xnq_probe_mfma_valu (int8 MFMA chains with independent VALU work)."""
+    check(_lib.load().xnq_probe_mfma_valu(int(valu_rounds), int(bool(split)), int(iters), int(workgroups), _ptr(sink),
+                                          _stream(sink.device)))
+
+
+def probe_lds_read(iters: int, workgroups: int, sink: torch.Tensor) -> None:
+    """Measurement hook xnq_probe_lds_read (conflict-free ds_read_b128 stream)."""
+    check(_lib.load().xnq_probe_lds_read(int(iters), int(workgroups), _ptr(sink), _stream(sink.device)))
+
+
 def set_route(route: int) -> None:
     """0 = route by m, 1 = force the matvec kernel, 2 = force the MFMA kernel."""
     check(_lib.load().xnq_set_route(int(route)))
