@@ -31,9 +31,9 @@ constexpr uint32_t kMaxLds = 160 * 1024;
 
 // LDS holds MB consecutive activation row images (ActImg in xnq_internal.h),
 // the same bytes as the quantized workspace, so staging is a flat copy.
-__host__ __device__ inline uint32_t lds_bytes(int mb, uint32_t k, bool kquant) {
-    return (uint32_t)mb * act_img(k, kquant).row_bytes;
-}
+// LDS bytes of MB staged rows: flat row images, or the interleaved layout of
+// the multi-row workspace path when that is larger
+__host__ __device__ inline uint32_t lds_bytes(int mb, uint32_t k, bool kquant);
 
 // Sum over the 64 lanes with DPP: row_shr 1/2/4/8 build each 16-lane row's
 // total in its last lane, row_bcast 15/31 carry it across rows; lane 63 ends
@@ -317,14 +317,18 @@ __device__ __forceinline__ void chunk_fma(const Chunk& ch, uint32_t c, const int
                                           float& acc) {
     const int bs0 = (int)(int16_t)(sv & 0xffff), bs1 = (int)(int16_t)(sv >> 16);
     if (DT == XNQ_Q4K) {
-        int sc, mn, lo, hi;
+        int sc, mn;
         const float dw = f16_bits_to_f32(ch.x.x), dmin = f16_bits_to_f32(ch.x.x >> 16);
         q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)(c & 7), sc, mn);
-        nib_dot2(ch.q, a, lo, hi);
-        // |lo + hi| <= 32*15*128 < 2^23: the 24-bit multiply is exact
-        const int isum = __mul24(sc, lo + hi);
-        const int msum = __mul24(mn, bs0 + bs1);
-        acc = fmaf(da, fmaf(dw, (float)isum, -(dmin * (float)msum)), acc);
+        const int raw = nib_dot(ch.q, a);  // |raw| <= 32*15*128
+        // dw * (sc * raw) with the integer product formed in f32: d (an
+        // f16, 11 significant bits) times sc (6 bits) is exact, and so is
+        // the integer |sc * raw| < 2^24, so cw * raw rounds the same
+        // exact product once, as the integer form does; the same holds for
+        // the min term.  cw and cm depend only on the chunk, so with several
+        // activation rows they are formed once.
+        const float cw = dw * (float)sc, cm = dmin * (float)mn;
+        acc = fmaf(da, fmaf(cw, (float)raw, -(cm * (float)(bs0 + bs1))), acc);
     } else if (DT == XNQ_Q6K) {
         const int sc0 = (int)(int8_t)(ch.x.z & 0xff), sc1 = (int)(int8_t)((ch.x.z >> 8) & 0xff);
         const int v = q6k_chunk_int(ch.q, make_uint2(ch.x.x, ch.x.y), a, sc0, sc1, bs0, bs1);
@@ -383,6 +387,55 @@ __device__ __forceinline__ void compute_chunk(const Chunk& ch, uint32_t c, uint3
     }
 }
 
+// Several activation rows (MB > 1, workspace path): the staged image is
+// interleaved by row in groups of 64 chunks (a wavefront's chunks of one
+// load instruction), so one chunk's reads for all MB rows sit at fixed
+// distances (immediate ds_read offsets, no per-row address arithmetic) and
+// the 64 lanes of one read still cover 64 consecutive slots (no bank
+// conflicts).  With chunk c = 64u + l, NU = ceil(nch / 64):
+//   [half 2][u NU][row MB][l 64][16]  quants: bytes 16h .. 16h+15 of chunk c
+//   [u NU][row MB][l 64] int32         side word of chunk c
+//   Q8K: [block nb][row MB] f32        d_a of block b (256 elements)
+//   Q8_0: [u NU][row MB][l 64] f32     d_a of chunk c
+struct IlLay {
+    uint32_t nu, sv, da, bytes;
+};
+__host__ __device__ inline IlLay il_lay(int mb, uint32_t k, bool kquant) {
+    IlLay L;
+    L.nu = (k / 32 + 63) / 64;
+    L.sv = 2 * L.nu * (uint32_t)mb * 1024;
+    L.da = L.sv + L.nu * (uint32_t)mb * 256;
+    L.bytes = L.da + (kquant ? (k / 256) * (uint32_t)mb * 4 : L.nu * (uint32_t)mb * 256);
+    return L;
+}
+
+__host__ __device__ inline uint32_t lds_bytes(int mb, uint32_t k, bool kquant) {
+    const uint32_t flat = (uint32_t)mb * act_img(k, kquant).row_bytes;
+    if (mb == 1) return flat;
+    const uint32_t il = il_lay(mb, k, kquant).bytes;
+    return il > flat ? il : flat;
+}
+
+template <int DT, int MB>
+__device__ __forceinline__ void compute_chunk_il(const Chunk& ch, uint32_t c, const IlLay& L,
+                                                 const uint8_t* lds, float* acc) {
+    const uint32_t u = c / 64, l = c % 64;
+    const uint8_t* q0 = lds + (u * MB * 64 + l) * 16;
+    const uint8_t* q1 = q0 + L.nu * (MB * 1024);
+    const int32_t* sv = reinterpret_cast<const int32_t*>(lds + L.sv) + u * MB * 64 + l;
+    const float* da = is_kquant(DT) ? reinterpret_cast<const float*>(lds + L.da) + (c >> 3) * MB
+                                    : reinterpret_cast<const float*>(lds + L.da) + u * MB * 64 + l;
+    constexpr uint32_t kDaStep = is_kquant(DT) ? 1 : 64;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const uint4 a0 = *reinterpret_cast<const uint4*>(q0 + mb * 1024);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(q1 + mb * 1024);
+        const int a[8] = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                          (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        chunk_fma<DT>(ch, c, a, sv[mb * 64], da[mb * kDaStep], acc[mb]);
+    }
+}
+
 // First staging batch of the quantized workspace, loaded into registers before
 // the weight loads are issued so its (L2) latency overlaps them.
 template <int MB, int NW>
@@ -398,6 +451,77 @@ struct StagePrefetch {
         for (int j = 0; j < kPer; j++) {
             const uint32_t i = j * NW * kWave + threadIdx.x;
             v[j] = src[min(min(i, total - 1), live - 1)];
+        }
+    }
+    // 16-byte piece i of the flat MB-row image, written to its place in the
+    // interleaved layout (compute_chunk_il)
+    __device__ __forceinline__ static void put_il(uint8_t* lds, const ActImg& A, const IlLay& L, bool kq,
+                                                  uint32_t r, uint32_t o, uint4 v) {
+        if (o < A.k) {
+            const uint32_t h = o >= A.k / 2 ? 1u : 0u;
+            const uint32_t c = (o - h * (A.k / 2)) / 16;
+            *reinterpret_cast<uint4*>(lds + (((h * L.nu + c / 64) * MB + r) * 64 + c % 64) * 16) = v;
+            return;
+        }
+        // side words and d_a, dword by dword (for short Q8_0 rows a piece
+        // can hold both: the regions are only dword aligned)
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t nch = A.k / 32, nb = kq ? A.k / 256 : nch;
+        uint32_t* sv = reinterpret_cast<uint32_t*>(lds + L.sv);
+        uint32_t* da = reinterpret_cast<uint32_t*>(lds + L.da);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t ob = o + 4 * j;
+            if (ob < A.d_off) {
+                const uint32_t c = (ob - A.s_off) / 4;
+                sv[((c / 64) * MB + r) * 64 + c % 64] = w[j];
+            } else {
+                const uint32_t b = (ob - A.d_off) / 4;
+                if (b < nb) {
+                    if (kq) da[b * MB + r] = w[j];
+                    else da[((b / 64) * MB + r) * 64 + b % 64] = w[j];
+                }
+            }
+        }
+    }
+    // Write the prefetched batch and copy whatever it did not cover, into the
+    // interleaved layout.
+    __device__ __forceinline__ void store_il(const AView& a, uint32_t m0, uint32_t mcount, const IlLay& L,
+                                             bool kq, uint8_t* lds) {
+        const uint32_t rb = a.A.row_bytes, rb16 = rb / 16;
+        const uint32_t total = (uint32_t)MB * rb16;
+        const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * rb16;
+        constexpr uint32_t kStep = NW * kWave;
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const uint32_t i = j * kStep + threadIdx.x;
+            // the prefetch clamped past-the-end lanes to the last live piece:
+            // rows past mcount only ever hold copies, never read for output
+            if (i < total) {
+                const uint32_t r = i / rb16;
+                put_il(lds, a.A, L, kq, r, (i - r * rb16) * 16, i < live ? v[j] : make_uint4(0u, 0u, 0u, 0u));
+            }
+        }
+        // the rest in batches of kBatch loads (one memory round trip per
+        // batch), walking (row, piece) without a division per piece
+        constexpr int kBatch = 4;
+        const uint4* src = reinterpret_cast<const uint4*>(a.img + (size_t)m0 * rb);
+        uint32_t i = kPer * kStep + threadIdx.x;
+        uint32_t r = i / rb16, p = i - r * rb16;
+        for (; i < total; i += kBatch * kStep) {
+            uint4 vb[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) vb[j] = src[min(i + j * kStep, live - 1)];
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const uint32_t ij = i + j * kStep;
+                if (ij < total) put_il(lds, a.A, L, kq, r, p * 16, ij < live ? vb[j] : make_uint4(0u, 0u, 0u, 0u));
+                p += kStep;
+                while (p >= rb16) {
+                    p -= rb16;
+                    r++;
+                }
+            }
         }
     }
     // Write the prefetched batch and copy whatever it did not cover.
@@ -429,7 +553,13 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
                                                          float* __restrict__ y) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr bool kq = is_kquant(DT);
+    // interleaved staging (compute_chunk_il): Q4_K from 4 rows (4096 -> 14336
+    // at m = 4: 14.0 against 14.7 us; 8192 -> 28672: 35 against 43).  At 2
+    // rows, and for Q6_K, its per-chunk address work outweighs the per-row
+    // savings (Q6_K 14336 -> 4096 at m = 2: 16.5 against 15.7).
+    constexpr bool kIL = MB >= 4 && !FUSED && DT == XNQ_Q4K;
     const ActImg A = act_img(w.k, kq);
+    const IlLay IL = il_lay(MB, w.k, kq);
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t nchunks = w.k / 32;
@@ -466,6 +596,8 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     if (FUSED) {
         xq.quant(lds, A, w.k, xq.first(wave), lane);
         xq.rest(x, w.k, m0, mcount, lds, A, wave, lane);
+    } else if (kIL) {
+        pre.store_il(a, m0, mcount, IL, kq, lds);
     } else {
         pre.store(a, m0, mcount, lds);
     }
@@ -485,7 +617,10 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
 #pragma unroll
                 for (int v = 0; v < CPL; v++) {
                     const uint32_t c = lane + 64 * (v + CPL * p);
-                    if (row < w.n && c < nchunks) compute_chunk<DT, MB>(ch[r][v], c, w.k, lds, A, acc[r]);
+                    if (row < w.n && c < nchunks) {
+                        if (kIL) compute_chunk_il<DT, MB>(ch[r][v], c, IL, lds, acc[r]);
+                        else compute_chunk<DT, MB>(ch[r][v], c, w.k, lds, A, acc[r]);
+                    }
                 }
             }
         }

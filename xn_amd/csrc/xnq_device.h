@@ -74,6 +74,20 @@ __device__ __forceinline__ void nib_dot2(uint4 q, const int* a, int& lo, int& hi
     hi = h;
 }
 
+// sum of q*a over the 32 nibbles of q (low nibbles against a[0..3], high
+// against a[4..7]) in one dependency chain
+__device__ __forceinline__ int nib_dot(uint4 q, const int* a) {
+    const uint32_t M = 0x0F0F0F0Fu;
+    int s = dot4((int)(q.x & M), a[0], 0);
+    s = dot4((int)(q.y & M), a[1], s);
+    s = dot4((int)(q.z & M), a[2], s);
+    s = dot4((int)(q.w & M), a[3], s);
+    s = dot4((int)((q.x >> 4) & M), a[4], s);
+    s = dot4((int)((q.y >> 4) & M), a[5], s);
+    s = dot4((int)((q.z >> 4) & M), a[6], s);
+    return dot4((int)((q.w >> 4) & M), a[7], s);
+}
+
 // Q4K: 6-bit scale and min of sub-block j from the 12 packed bytes
 // (utils.rs:53-63 get_scale_min_k4); s0,s1,s2 = scales bytes 0-3, 4-7, 8-11.
 __device__ __forceinline__ uint32_t byte_of3(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
