@@ -387,52 +387,55 @@ __device__ __forceinline__ void compute_chunk(const Chunk& ch, uint32_t c, uint3
     }
 }
 
-// Several activation rows (MB > 1, workspace path): the staged image is
-// interleaved by row in groups of 64 chunks (a wavefront's chunks of one
+// Q4_K with several activation rows (MB >= 4, workspace path): the staged
+// Q8K image is interleaved by row in groups of 64 chunks (a wavefront's chunks of one
 // load instruction), so one chunk's reads for all MB rows sit at fixed
 // distances (immediate ds_read offsets, no per-row address arithmetic) and
 // the 64 lanes of one read still cover 64 consecutive slots (no bank
 // conflicts).  With chunk c = 64u + l, NU = ceil(nch / 64):
 //   [half 2][u NU][row MB][l 64][16]  quants: bytes 16h .. 16h+15 of chunk c
-//   [u NU][row MB][l 64] int32         side word of chunk c
-//   Q8K: [block nb][row MB] f32        d_a of block b (256 elements)
-//   Q8_0: [u NU][row MB][l 64] f32     d_a of chunk c
+//   [u NU][row MB][l 64] f32           chunk c's bsum (both 16-element halves)
+//   [block nb][row MB] f32             d_a of block b (256 elements)
 struct IlLay {
     uint32_t nu, sv, da, bytes;
 };
-__host__ __device__ inline IlLay il_lay(int mb, uint32_t k, bool kquant) {
+__host__ __device__ inline IlLay il_lay(int mb, uint32_t k) {
     IlLay L;
     L.nu = (k / 32 + 63) / 64;
     L.sv = 2 * L.nu * (uint32_t)mb * 1024;
     L.da = L.sv + L.nu * (uint32_t)mb * 256;
-    L.bytes = L.da + (kquant ? (k / 256) * (uint32_t)mb * 4 : L.nu * (uint32_t)mb * 256);
+    L.bytes = L.da + (k / 256) * (uint32_t)mb * 4;
     return L;
 }
 
 __host__ __device__ inline uint32_t lds_bytes(int mb, uint32_t k, bool kquant) {
     const uint32_t flat = (uint32_t)mb * act_img(k, kquant).row_bytes;
     if (mb == 1) return flat;
-    const uint32_t il = il_lay(mb, k, kquant).bytes;
+    const uint32_t il = kquant ? il_lay(mb, k).bytes : 0u;
     return il > flat ? il : flat;
 }
 
 template <int DT, int MB>
 __device__ __forceinline__ void compute_chunk_il(const Chunk& ch, uint32_t c, const IlLay& L,
                                                  const uint8_t* lds, float* acc) {
+    static_assert(DT == XNQ_Q4K, "the interleaved staging holds Q4_K's f32 chunk bsums");
+    int sc, mn;
+    q4k_scale_min(ch.x.y, ch.x.z, ch.x.w, (int)(c & 7), sc, mn);
+    const float cw = f16_bits_to_f32(ch.x.x) * (float)sc, cm = f16_bits_to_f32(ch.x.x >> 16) * (float)mn;
     const uint32_t u = c / 64, l = c % 64;
     const uint8_t* q0 = lds + (u * MB * 64 + l) * 16;
     const uint8_t* q1 = q0 + L.nu * (MB * 1024);
-    const int32_t* sv = reinterpret_cast<const int32_t*>(lds + L.sv) + u * MB * 64 + l;
-    const float* da = is_kquant(DT) ? reinterpret_cast<const float*>(lds + L.da) + (c >> 3) * MB
-                                    : reinterpret_cast<const float*>(lds + L.da) + u * MB * 64 + l;
-    constexpr uint32_t kDaStep = is_kquant(DT) ? 1 : 64;
+    const float* sv = reinterpret_cast<const float*>(lds + L.sv) + u * MB * 64 + l;
+    const float* da = reinterpret_cast<const float*>(lds + L.da) + (c >> 3) * MB;
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const uint4 a0 = *reinterpret_cast<const uint4*>(q0 + mb * 1024);
         const uint4 a1 = *reinterpret_cast<const uint4*>(q1 + mb * 1024);
         const int a[8] = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                           (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        chunk_fma<DT>(ch, c, a, sv[mb * 64], da[mb * kDaStep], acc[mb]);
+        // chunk_fma's Q4K combine with the bsum already summed in f32
+        const int raw = nib_dot(ch.q, a);
+        acc[mb] = fmaf(da[mb], fmaf(cw, (float)raw, -(cm * sv[mb * 64])), acc[mb]);
     }
 }
 
@@ -455,18 +458,17 @@ struct StagePrefetch {
     }
     // 16-byte piece i of the flat MB-row image, written to its place in the
     // interleaved layout (compute_chunk_il)
-    __device__ __forceinline__ static void put_il(uint8_t* lds, const ActImg& A, const IlLay& L, bool kq,
-                                                  uint32_t r, uint32_t o, uint4 v) {
+    __device__ __forceinline__ static void put_il(uint8_t* lds, const ActImg& A, const IlLay& L, uint32_t r,
+                                                  uint32_t o, uint4 v) {
         if (o < A.k) {
             const uint32_t h = o >= A.k / 2 ? 1u : 0u;
             const uint32_t c = (o - h * (A.k / 2)) / 16;
             *reinterpret_cast<uint4*>(lds + (((h * L.nu + c / 64) * MB + r) * 64 + c % 64) * 16) = v;
             return;
         }
-        // side words and d_a, dword by dword (for short Q8_0 rows a piece
-        // can hold both: the regions are only dword aligned)
+        // side words and d_a, dword by dword
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        const uint32_t nch = A.k / 32, nb = kq ? A.k / 256 : nch;
+        const uint32_t nb = A.k / 256;
         uint32_t* sv = reinterpret_cast<uint32_t*>(lds + L.sv);
         uint32_t* da = reinterpret_cast<uint32_t*>(lds + L.da);
 #pragma unroll
@@ -474,20 +476,19 @@ struct StagePrefetch {
             const uint32_t ob = o + 4 * j;
             if (ob < A.d_off) {
                 const uint32_t c = (ob - A.s_off) / 4;
-                sv[((c / 64) * MB + r) * 64 + c % 64] = w[j];
+                // the chunk's two 16-element bsums, summed, as f32 (exact)
+                const float bsum = (float)((int)(int16_t)(w[j] & 0xffffu) + (int)(int16_t)(w[j] >> 16));
+                sv[((c / 64) * MB + r) * 64 + c % 64] = __float_as_uint(bsum);
             } else {
                 const uint32_t b = (ob - A.d_off) / 4;
-                if (b < nb) {
-                    if (kq) da[b * MB + r] = w[j];
-                    else da[((b / 64) * MB + r) * 64 + b % 64] = w[j];
-                }
+                if (b < nb) da[b * MB + r] = w[j];
             }
         }
     }
     // Write the prefetched batch and copy whatever it did not cover, into the
     // interleaved layout.
     __device__ __forceinline__ void store_il(const AView& a, uint32_t m0, uint32_t mcount, const IlLay& L,
-                                             bool kq, uint8_t* lds) {
+                                             uint8_t* lds) {
         const uint32_t rb = a.A.row_bytes, rb16 = rb / 16;
         const uint32_t total = (uint32_t)MB * rb16;
         const uint32_t live = (mcount < (uint32_t)MB ? mcount : MB) * rb16;
@@ -499,7 +500,7 @@ struct StagePrefetch {
             // rows past mcount only ever hold copies, never read for output
             if (i < total) {
                 const uint32_t r = i / rb16;
-                put_il(lds, a.A, L, kq, r, (i - r * rb16) * 16, i < live ? v[j] : make_uint4(0u, 0u, 0u, 0u));
+                put_il(lds, a.A, L, r, (i - r * rb16) * 16, i < live ? v[j] : make_uint4(0u, 0u, 0u, 0u));
             }
         }
         // the rest in batches of kBatch loads (one memory round trip per
@@ -515,7 +516,7 @@ struct StagePrefetch {
 #pragma unroll
             for (int j = 0; j < kBatch; j++) {
                 const uint32_t ij = i + j * kStep;
-                if (ij < total) put_il(lds, a.A, L, kq, r, p * 16, ij < live ? vb[j] : make_uint4(0u, 0u, 0u, 0u));
+                if (ij < total) put_il(lds, a.A, L, r, p * 16, ij < live ? vb[j] : make_uint4(0u, 0u, 0u, 0u));
                 p += kStep;
                 while (p >= rb16) {
                     p -= rb16;
@@ -559,7 +560,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     // savings (Q6_K 14336 -> 4096 at m = 2: 16.5 against 15.7).
     constexpr bool kIL = MB >= 4 && !FUSED && DT == XNQ_Q4K;
     const ActImg A = act_img(w.k, kq);
-    const IlLay IL = il_lay(MB, w.k, kq);
+    const IlLay IL = il_lay(MB, w.k);
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t nchunks = w.k / 32;
@@ -596,8 +597,8 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     if (FUSED) {
         xq.quant(lds, A, w.k, xq.first(wave), lane);
         xq.rest(x, w.k, m0, mcount, lds, A, wave, lane);
-    } else if (kIL) {
-        pre.store_il(a, m0, mcount, IL, kq, lds);
+    } else if constexpr (kIL) {
+        pre.store_il(a, m0, mcount, IL, lds);
     } else {
         pre.store(a, m0, mcount, lds);
     }
@@ -618,7 +619,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
                 for (int v = 0; v < CPL; v++) {
                     const uint32_t c = lane + 64 * (v + CPL * p);
                     if (row < w.n && c < nchunks) {
-                        if (kIL) compute_chunk_il<DT, MB>(ch[r][v], c, IL, lds, acc[r]);
+                        if constexpr (kIL) compute_chunk_il<DT, MB>(ch[r][v], c, IL, lds, acc[r]);
                         else compute_chunk<DT, MB>(ch[r][v], c, w.k, lds, A, acc[r]);
                     }
                 }
