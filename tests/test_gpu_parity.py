@@ -196,6 +196,29 @@ def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
     assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(4, 301, 2304), (5, 77, 768), (7, 130, 8448), (8, 257, 256), (12, 99, 2304),
+                                   (16, 64, 4096)])
+def test_matmul_q4k_multirow_matvec(orc, dev, m, n, k):
+    """Q4_K on the matvec route (forced) from 4 rows, where the staged
+    activation image is interleaved by row in groups of 64 chunks: K whose
+    chunk count is not a multiple of 64, rows past the launch's 4 or 8, and
+    m above 8 (a second launch)."""
+    from xn_amd.quantized import set_route
+
+    rng = np.random.default_rng(8300 + m + n + k)
+    blocks = orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, Q4K, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    set_route(1)
+    try:
+        # quantize_lhs + matmul_preq: the workspace (non-fused) matvec kernels
+        qt.matmul_t_split((m, k, n), torch.from_numpy(x).to(dev), dst)
+    finally:
+        set_route(0)
+    assert_close(dst.cpu().numpy(), orc.matmul(Q4K, x, blocks, n), f"m={m} n={n} k={k}")
+
+
 @pytest.mark.parametrize("dt", [Q4K, Q6K])
 @pytest.mark.parametrize("m,n,k", [(2, 300, 2048), (5, 129, 768), (8, 512, 4096), (16, 200, 1024),
                                    (31, 384, 2304), (33, 256, 1280), (64, 130, 512)])
