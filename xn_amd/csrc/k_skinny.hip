@@ -35,6 +35,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef short v2s __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -55,22 +56,26 @@ template <int DT, int MT, int NW>
 struct KLay {
     static constexpr bool kQ4K = DT == XNQ_Q4K;
     static constexpr int kWaves = NW, kThreads = 64 * NW, kCols = 32 * NW;
-    static constexpr int R = 32 * MT;
+    static constexpr int R = MT == 0 ? 16 : 32 * MT;
     static constexpr int kWq = 0;
     static constexpr int kHdr = kWq + kCols * 128;
     static constexpr int kWh = kHdr + kWaves * 64 * 16;
     static constexpr int kWd = kWh + (kQ4K ? 0 : kCols * 64);
     static constexpr int kAct = kWd + (kQ4K ? 0 : kWaves * 64 * 4);
     static constexpr int kBs = kAct + 8 * 2 * R * 16;
-    static constexpr int kDa = kBs + (kQ4K ? R * 32 : 0);
+    static constexpr int kDa = kBs + (kQ4K ? (R < 32 ? 32 : R) * 32 : 0);  // one DMA fills 32 rows
     static constexpr int kDummy = kDa + 64 * 4;  // target of the padding DMA
-    static constexpr int kSlot = kDummy + 64 * 4;
+    // MT == 0 with 8 wavefronts: the 4 KiB activation tile takes 4 of them,
+    // the other 4 issue the same load into this scratch piece
+    static constexpr int kDummyAct = kDummy + 64 * 4;
+    static constexpr int kSlot = kDummyAct + (MT == 0 && NW == 8 ? 1024 : 0);
     static constexpr int kRing = (4 * kSlot <= 160 * 1024) ? 4 : (3 * kSlot <= 160 * 1024) ? 3 : 2;
     static constexpr int kLds = kRing * kSlot;
     // DMA instructions per wavefront per super-block, the same in every
     // wavefront so one vmcnt count fits all: weights, activation pieces, and
     // one of {bsums, d_a, padding}
-    static constexpr int kActPer = 8 * MT / NW;  // 8 * MT KiB of activation over NW wavefronts
+    // 8 * MT KiB of activation over NW wavefronts (MT == 0: 4 KiB, one each)
+    static constexpr int kActPer = MT == 0 ? 1 : 8 * MT / NW;
     static constexpr int kWPer = kQ4K ? 4 + 1 : 4 + 1 + 2 + 1;
     static constexpr int kD = kWPer + kActPer + 1;
     static_assert(kLds <= 160 * 1024, "LDS budget");
@@ -128,6 +133,115 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
     return make_uint4(hu.x, hu.y, lu.x, lu.y);
 }
 
+// One super-block of a 16-row tile (m <= 16) for wavefront `wave`'s 32
+// columns, as two 16-column tiles on v_mfma_i32_16x16x64_i8: lane l holds
+// row / column l & 15 and the 16-element K slice g = l >> 4 of each
+// 64-element step, that is half g & 1 of chunk 2*ks + (g >> 1); the
+// accumulator holds rows 4g .. 4g+3 of column l & 15.  Digit planes,
+// epilogue and min term as in the 32-row path (skinny_kernel).
+template <int DT, int NW>
+__device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint32_t lane, bool odd_sb, v4f* acc) {
+    using L = KLay<DT, 0, NW>;
+    constexpr bool kQ4K = L::kQ4K;
+    constexpr int kShift = kQ4K ? 3 : 7;
+    const uint32_t g = lane >> 4, li = lane & 15, h = g & 1;
+    uint4 hdr[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++)
+        hdr[ct] = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 64 + ct * 16 + li) * 16);
+    v4i hi[2], lo[2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const int c = 2 * ks + (int)(g >> 1);
+        const v4i av = *reinterpret_cast<const v4i*>(S + L::kAct + ((4 * ks + g) * 16 + li) * 16);
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            const uint32_t cl = wave * 32 + ct * 16 + li;
+            const uint4 qc = *reinterpret_cast<const uint4*>(S + L::kWq + cl * 128 + ((c ^ (cl & 7)) * 16));
+            const uint32_t q4[4] = {qc.x, qc.y, qc.z, qc.w};
+            uint32_t p0[4], p1[4];
+            if (kQ4K) {
+                int sc, mn;
+                q4k_scale_min(hdr[ct].y, hdr[ct].z, hdr[ct].w, c, sc, mn);
+                const uint32_t sh = (uint32_t)sc >> 3, sl = (uint32_t)sc & 7;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t nib = (q4[j] >> (4 * h)) & 0x0F0F0F0Fu;
+                    p0[j] = mul_bytes(nib, sh);
+                    p1[j] = mul_bytes(nib, sl);
+                }
+            } else {
+                const uint2 qh = *reinterpret_cast<const uint2*>(S + L::kWh + cl * 64 + (((c >> 1) ^ (cl & 3)) * 16) +
+                                                                 (c & 1) * 8);
+                const uint32_t qhw = h ? qh.y : qh.x;
+                const uint32_t hw = hdr[ct].x, hy = hdr[ct].y, hz = hdr[ct].z, hv = hdr[ct].w;
+                const uint32_t sw = (c >> 1) == 0 ? hw : (c >> 1) == 1 ? hy : (c >> 1) == 2 ? hz : hv;
+                const int sc = (int)(int8_t)(sw >> (8 * (2 * (c & 1) + h)));
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t b = ((q4[j] >> (4 * h)) & 0x0F0F0F0Fu) | (((qhw >> (2 * j)) & 0x03030303u) << 4);
+                    q6_digits(b, sc, p1[j], p0[j]);
+                }
+            }
+            const v4i b0 = {(int)p0[0], (int)p0[1], (int)p0[2], (int)p0[3]};
+            const v4i b1 = {(int)p1[0], (int)p1[1], (int)p1[2], (int)p1[3]};
+            if (ks == 0) {
+                hi[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b0, v4i{}, 0, 0, 0);
+                lo[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b1, v4i{}, 0, 0, 0);
+            } else {
+                hi[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b0, hi[ct], 0, 0, 0);
+                lo[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b1, lo[ct], 0, 0, 0);
+            }
+        }
+    }
+    // epilogue: acc += d_a d_w (hi * 2^s + lo)  [- d_a dmin sum_j m_j bsum32_j]
+    const float* eda = reinterpret_cast<const float*>(S + L::kDa);
+    const float4 d4 = *reinterpret_cast<const float4*>(eda + 4 * g);
+    const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+    v8bf a8;
+    if (kQ4K) {
+        // row side of the min term: -d_a * bsum32 of sub-blocks 2g, 2g+1 of row li,
+        // as bf16 hi/lo pairs (ah0, al0, ah1, al1) twice
+        const uint2 pr = *reinterpret_cast<const uint2*>(S + L::kBs + (li * 2 + (g >> 1)) * 16 + (g & 1) * 8);
+        const float dr = eda[li];
+        float v[2];
+        v[0] = -dr * (float)((int)(int16_t)(pr.x & 0xffffu) + (int)(int16_t)(pr.x >> 16));
+        v[1] = -dr * (float)((int)(int16_t)(pr.y & 0xffffu) + (int)(int16_t)(pr.y >> 16));
+        const __bf16 h0 = (__bf16)v[0], h1 = (__bf16)v[1];
+        const __bf16 l0 = (__bf16)(v[0] - (float)h0), l1 = (__bf16)(v[1] - (float)h1);
+        a8 = v8bf{h0, l0, h1, l1, h0, l0, h1, l1};
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++) {
+        float dw;
+        if (kQ4K) {
+            dw = f16_bits_to_f32(hdr[ct].x & 0xffffu);
+        } else {
+            const uint32_t dd = reinterpret_cast<const uint32_t*>(S + L::kWd)[wave * 64 + ct * 16 + li];
+            dw = f16_bits_to_f32(odd_sb ? (dd >> 16) : (dd & 0xffffu));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int iv = hi[ct][e] * (1 << kShift) + lo[ct][e];
+            acc[ct][e] = fmaf((float)iv, dw * da[e], acc[ct][e]);
+        }
+        if (kQ4K) {
+            // column side: dmin * m_j of sub-blocks 2g, 2g+1, hi/lo bf16 pairs
+            // (mh0, mh0, mh1, mh1, ml0, ml0, ml1, ml1): the 8-term dot with a8
+            // is (ah0 + al0)(mh0 + ml0) + (ah1 + al1)(mh1 + ml1)
+            const float dm = f16_bits_to_f32(hdr[ct].x >> 16);
+            int sc0, mn0, sc1, mn1;
+            q4k_scale_min(hdr[ct].y, hdr[ct].z, hdr[ct].w, (int)(2 * g), sc0, mn0);
+            q4k_scale_min(hdr[ct].y, hdr[ct].z, hdr[ct].w, (int)(2 * g + 1), sc1, mn1);
+            const float w0 = dm * (float)mn0, w1 = dm * (float)mn1;
+            const __bf16 h0 = (__bf16)w0, h1 = (__bf16)w1;
+            const __bf16 l0 = (__bf16)(w0 - (float)h0), l1 = (__bf16)(w1 - (float)h1);
+            const v8bf b8 = {h0, h0, h1, h1, l0, l0, l1, l1};
+            acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8, b8, acc[ct], 0, 0, 0);
+        }
+    }
+}
+
 // Where each weight of a launch writes: y[t] (the destination, or its
 // split-K partial region of `stride[t]` floats per split) for the column
 // tiles below tile_end[t] (cumulative over the group).
@@ -168,7 +282,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     // those outputs are dropped at the store
     const uint32_t cmax = w.n - 1, rmax = m - 1;
     // Q4K: bsums take the first MT wavefronts' extra instruction, d_a the next
-    constexpr uint32_t kExtraBs = kQ4K ? (uint32_t)MT : 0u;
+    constexpr uint32_t kExtraBs = kQ4K ? (uint32_t)(MT == 0 ? 1 : MT) : 0u;
 
     // ---- the DMA of super-block i: kD instructions per wavefront ----
     // Per-lane byte offsets are fixed for the whole walk; the super-block
@@ -194,14 +308,15 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     }
     // activation pieces of 1 KiB.  MT == 1: piece = chunk c, lanes 0-31 rows
     // of half 0, lanes 32-63 rows of half 1.  MT == 2: piece = (chunk, half),
-    // lane = row.
+    // lane = row.  MT == 0: four 16-row (chunk, half) pieces p = 4w + lane/16
+    // (wavefront w & 3), lane & 15 = row.
     uint32_t oa[L::kActPer];
 #pragma unroll
     for (int j = 0; j < L::kActPer; j++) {
-        const uint32_t t = wave * L::kActPer + j;
+        const uint32_t t = MT == 0 ? (wave & 3) * 4 + (lane >> 4) : wave * L::kActPer + j;
         const uint32_t c = MT == 1 ? t : t >> 1;
         const uint32_t hsel = MT == 1 ? half : (t & 1);
-        const uint32_t row = MT == 1 ? lrow : lane;
+        const uint32_t row = MT == 1 ? lrow : MT == 0 ? (lane & 15) : lane;
         oa[j] = min(row, rmax) * A.row_bytes + hsel * (A.k / 2) + c * 16;
     }
     // the extra instruction: Q4K bsums (rows 32*wave .. +31), d_a, or padding
@@ -219,21 +334,27 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
             for (int j = 0; j < 2; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + (wave * 32 + 16 * j) * 64);
             dma4(w.d + (sb & ~1u) * 2, od, slot + L::kWd + wave * 64 * 4);
         }
+        if (MT == 0) {
+            dma16(a.img + sb * 128, oa[0], slot + (wave < 4 ? L::kAct + wave * 1024 : L::kDummyAct));
+        } else {
 #pragma unroll
-        for (int j = 0; j < L::kActPer; j++) {
-            const uint32_t t = wave * L::kActPer + j;
-            const uint32_t c = MT == 1 ? t : t >> 1;
-            const uint32_t hsel = MT == 1 ? 0u : (t & 1);
-            dma16(a.img + sb * 128, oa[j], slot + L::kAct + (c * 2 + hsel) * L::R * 16);
+            for (int j = 0; j < L::kActPer; j++) {
+                const uint32_t t = wave * L::kActPer + j;
+                const uint32_t c = MT == 1 ? t : t >> 1;
+                const uint32_t hsel = MT == 1 ? 0u : (t & 1);
+                dma16(a.img + sb * 128, oa[j], slot + L::kAct + (c * 2 + hsel) * L::R * 16);
+            }
         }
         if (wave < kExtraBs) dma16(a.img + sb * 32, obs, slot + L::kBs + wave * 32 * 32);
         else if (wave == kExtraBs) dma4(a.img + sb * 4, oda, slot + L::kDa);
         else dma4(a.img + sb * 4, oda, slot + L::kDummy);
     };
 
-    v16f acc[MT];
+    constexpr int kAccT = MT == 0 ? 1 : MT;
+    v16f acc[kAccT];
 #pragma unroll
-    for (int t = 0; t < MT; t++) acc[t] = v16f{};
+    for (int t = 0; t < kAccT; t++) acc[t] = v16f{};
+    v4f acc16[2] = {v4f{}, v4f{}};  // MT == 0: the two 16-column tiles
 
     // prologue: super-blocks 0 .. kRing-2 in flight
 #pragma unroll
@@ -250,6 +371,9 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
         if (i + kRing - 1 < nsb) issue(i + kRing - 1);
 
         const uint8_t* S = lds + (i % kRing) * L::kSlot;
+        if constexpr (MT == 0) {
+            compute16<DT, NW>(S, wave, lane, ((sb0 + i) & 1) != 0, acc16);
+        } else {
         const uint32_t cl = wave * 32 + lrow;
         const uint4 hdr = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 64 + lrow) * 16);
         v16i hi[MT], lo[MT];
@@ -348,8 +472,24 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bl8, acc[t], 0, 0, 0);
             }
         }
+        }  // MT >= 1
     }
 
+    if constexpr (MT == 0) {
+        const uint32_t g = lane >> 4;
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            const uint32_t col = col0 + wave * 32 + ct * 16 + (lane & 15);
+            if (col < w.n) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t row = 4 * g + e;
+                    if (row < m) y[(size_t)row * w.n + col] = acc16[ct][e];
+                }
+            }
+        }
+        return;
+    }
     if (ncol < w.n) {
 #pragma unroll
         for (int t = 0; t < MT; t++)
@@ -427,6 +567,16 @@ uint32_t skinny_splits(size_t m, size_t n, size_t k) {
     return splits < 1 ? 1u : (uint32_t)splits;
 }
 
+// 16-row tiles on the 16x16x64 matrix-core op for m <= 16 (XNQ_SKINNY16=0
+// keeps the 32-row tiles; tuning)
+static bool skinny16() {
+    static const bool on = [] {
+        const char* e = getenv("XNQ_SKINNY16");
+        return !e || atoi(e) != 0;
+    }();
+    return on;
+}
+
 bool skinny_supported(uint32_t dtype, size_t m, size_t n, size_t k) {
     (void)n;
     return (dtype == XNQ_Q4K || dtype == XNQ_Q6K) && k % 256 == 0 && m >= 1 && m <= 64;
@@ -443,6 +593,9 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
     const bool w8 = skinny_waves(m, n, G.w[0].k) == 8;
 #define XNQ_SK(DT)                                                                                   \
     if (G.w[0].dtype == DT) {                                                                        \
+        if (m <= 16 && skinny16())                                                                 \
+            return w8 ? launch_skinny_dt<DT, 0, 8>(G, a, m, splits, partial, silu, s)               \
+                      : launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s);              \
         if (m <= 32)                                                                                 \
             return w8 ? launch_skinny_dt<DT, 1, 8>(G, a, m, splits, partial, silu, s)               \
                       : launch_skinny_dt<DT, 1, 4>(G, a, m, splits, partial, silu, s);              \
