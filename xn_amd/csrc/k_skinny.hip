@@ -52,6 +52,11 @@ typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 //   da   [64] f32 d_a per row (rows past m repeat the last)
 // The XOR slot order makes the 32 columns' reads of one chunk hit distinct
 // banks while each column's bytes still arrive as one 128-byte line.
+#ifndef XNQ_SKINNY_RING_MAX
+#define XNQ_SKINNY_RING_MAX 4
+#endif
+constexpr int kRingMax = XNQ_SKINNY_RING_MAX;
+
 template <int DT, int MT, int NW>
 struct KLay {
     static constexpr bool kQ4K = DT == XNQ_Q4K;
@@ -69,7 +74,10 @@ struct KLay {
     // the other 4 issue the same load into this scratch piece
     static constexpr int kDummyAct = kDummy + 64 * 4;
     static constexpr int kSlot = kDummyAct + (MT == 0 && NW == 8 ? 1024 : 0);
-    static constexpr int kRing = (4 * kSlot <= 160 * 1024) ? 4 : (3 * kSlot <= 160 * 1024) ? 3 : 2;
+    static constexpr int kRing = (kRingMax * kSlot <= 160 * 1024) ? kRingMax
+                                 : (4 * kSlot <= 160 * 1024)        ? 4
+                                 : (3 * kSlot <= 160 * 1024)        ? 3
+                                                                    : 2;
     static constexpr int kLds = kRing * kSlot;
     // DMA instructions per wavefront per super-block, the same in every
     // wavefront so one vmcnt count fits all: weights, activation pieces, and
@@ -79,7 +87,7 @@ struct KLay {
     static constexpr int kWPer = kQ4K ? 4 + 1 : 4 + 1 + 2 + 1;
     static constexpr int kD = kWPer + kActPer + 1;
     static_assert(kLds <= 160 * 1024, "LDS budget");
-    static_assert(2 * kD < 64, "vmcnt range");
+    static_assert((kRing - 2) * kD < 64, "vmcnt range");
 };
 
 // global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
@@ -98,6 +106,18 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until at most `younger` super-blocks' DMA (KD instructions each) are
+// outstanding, younger <= Y (wavefront-uniform).
+template <int KD, int Y>
+__device__ __forceinline__ void wait_younger(uint32_t younger) {
+    if constexpr (Y == 0) {
+        wait_vm<0>();
+    } else {
+        if (younger >= (uint32_t)Y) wait_vm<Y * KD>();
+        else wait_younger<KD, Y - 1>(younger);
+    }
 }
 
 // bytes of d (each <= 15) times s (<= 7): one packed 16-bit multiply
@@ -364,9 +384,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     for (uint32_t i = 0; i < nsb; i++) {
         // wait for super-block i: the younger ones in flight are i+1 .. i+kRing-2
         const uint32_t younger = min((uint32_t)(kRing - 2), nsb - 1 - i);
-        if (kRing >= 4 && younger >= 2) wait_vm<2 * kD>();
-        else if (kRing >= 3 && younger >= 1) wait_vm<kD>();
-        else wait_vm<0>();
+        wait_younger<kD, kRing - 2>(younger);
         __syncthreads();  // every wavefront's DMA of i landed; slot (i-1) % kRing is free
         if (i + kRing - 1 < nsb) issue(i + kRing - 1);
 
