@@ -187,6 +187,10 @@ def sweep(args, dev, stream, gen) -> dict:
         matvec_row("5 q6k ffn down", 14, 14336, 4096, [1, 4])
         matvec_row("2 q4_0 gate/up", 2, 4096, 14336, [1])
         matvec_row("2 q4_0 down", 2, 14336, 4096, [1])
+        # one GPU's shard of an 8-way split FFN: gate/up column-parallel
+        # (4096 -> 14336/8), down row-parallel (K = 14336/8 = 7 super-blocks)
+        matvec_row("e shard/8 q4k gate/up (column-parallel)", 12, 4096, 1792, [1, 16])
+        matvec_row("e shard/8 q6k down (row-parallel)", 14, 1792, 4096, [1, 16])
 
     # config 2: Q4_0 FFN block, h = silu(x Wg^T) * (x Wu^T), y = h Wd^T
     k, f = 4096, 14336

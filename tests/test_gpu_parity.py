@@ -160,6 +160,8 @@ def test_matmul_small(orc, dev, dt, m, entry):
     (Q4K, 4096, 14336),
     (Q4K, 14336, 4096),
     (Q6K, 14336, 4096),   # config 5 FFN down
+    (Q4K, 4096, 1792),    # an 8-way column-parallel shard of gate/up
+    (Q6K, 1792, 4096),    # an 8-way row-parallel shard of down
 ])
 @pytest.mark.parametrize("m", [1, 4, 8])  # m = 8: matvec for Q6_K and 4096 x 4096, skinny for Q4_K K = 14336
 def test_matmul_config_shapes(orc, dev, dt, k, n, m):
