@@ -427,3 +427,35 @@ def test_stream_read_folds_every_word(dev, nbytes):
     torch.cuda.synchronize()
     want = np.bitwise_xor.reduce(host)
     assert int(sink.cpu().numpy().view(np.uint32)[0]) == int(want)
+
+
+
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
+@pytest.mark.parametrize("m", [9, 16, 40])
+def test_skinny_split_k_back_to_back(orc, dev, dt, m):
+    """Split-K skinny calls that share one workspace (activation image and
+    partial sums), six queued back to back with different activations and no
+    host synchronisation, plain and SiLU-gated, each checked against the
+    oracle."""
+    from xn_amd.quantized import matmul_t_silu_gate
+
+    k, n = 4096, 1280
+    rng = np.random.default_rng(8700 + dt + m)
+    wb = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    ub = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    w, u = upload(wb, n, k, dt, dev), upload(ub, n, k, dt, dev)
+    xs = [rng.normal(0, 1, (m, k)).astype(np.float32) for _ in range(6)]
+    ws = torch.empty(max(w.matmul_t_workspace_size(m), 1), dtype=torch.uint8, device=dev)
+    outs, gated = [], []
+    for x in xs:
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        w.matmul_t_ws((m, k, n), torch.from_numpy(x).to(dev), ws, y)
+        outs.append(y)
+        h = torch.empty((m, n), dtype=torch.float32, device=dev)
+        matmul_t_silu_gate(w, u, (m, k, n), torch.from_numpy(x).to(dev), h)
+        gated.append(h)
+    for i, x in enumerate(xs):
+        want = orc.matmul(dt, x, wb, n)
+        assert_close(outs[i].cpu().numpy(), want, f"call {i} dt={dt} m={m}")
+        want_h = _silu(want.astype(np.float64)) * orc.matmul(dt, x, ub, n)
+        assert_close(gated[i].cpu().numpy(), want_h, f"gated call {i} dt={dt} m={m}")
