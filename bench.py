@@ -339,7 +339,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(multi-GPU sharding is described in DESIGN.md, not implemented)"}))
+                          "(sharding the weights across GPUs is not built; --only sweep times one GPU's "
+                          "shard of an 8-way split FFN at its real shape)"}))
         sys.exit(2)
 
     import torch
