@@ -62,18 +62,19 @@ struct KLay {
     static constexpr bool kQ4K = DT == XNQ_Q4K;
     static constexpr int kWaves = NW, kThreads = 64 * NW, kCols = 32 * NW;
     static constexpr int R = MT == 0 ? 16 : 32 * MT;
+    // 16-row tiles: headers and Q6K d once per column ([col][16], [col]
+    // dword), fetched by the first kCols / 64 wavefronts, and no padding DMA
+    static constexpr bool kNarrow = MT == 0;
+    static constexpr int kHdrWaves = kCols / 64;
     static constexpr int kWq = 0;
     static constexpr int kHdr = kWq + kCols * 128;
-    static constexpr int kWh = kHdr + kWaves * 64 * 16;
+    static constexpr int kWh = kHdr + (kNarrow ? kCols * 16 : kWaves * 64 * 16);
     static constexpr int kWd = kWh + (kQ4K ? 0 : kCols * 64);
-    static constexpr int kAct = kWd + (kQ4K ? 0 : kWaves * 64 * 4);
+    static constexpr int kAct = kWd + (kQ4K ? 0 : (kNarrow ? kCols * 4 : kWaves * 64 * 4));
     static constexpr int kBs = kAct + 8 * 2 * R * 16;
     static constexpr int kDa = kBs + (kQ4K ? (R < 32 ? 32 : R) * 32 : 0);  // one DMA fills 32 rows
     static constexpr int kDummy = kDa + 64 * 4;  // target of the padding DMA
-    // MT == 0 with 8 wavefronts: the 4 KiB activation tile takes 4 of them,
-    // the other 4 issue the same load into this scratch piece
-    static constexpr int kDummyAct = kDummy + 64 * 4;
-    static constexpr int kSlot = kDummyAct + (MT == 0 && NW == 8 ? 1024 : 0);
+    static constexpr int kSlot = kDummy + (kNarrow ? 0 : 64 * 4);
     static constexpr int kRing = (kRingMax * kSlot <= 160 * 1024) ? kRingMax
                                  : (4 * kSlot <= 160 * 1024)        ? 4
                                  : (3 * kSlot <= 160 * 1024)        ? 3
@@ -85,9 +86,17 @@ struct KLay {
     // 8 * MT KiB of activation over NW wavefronts (MT == 0: 4 KiB, one each)
     static constexpr int kActPer = MT == 0 ? 1 : 8 * MT / NW;
     static constexpr int kWPer = kQ4K ? 4 + 1 : 4 + 1 + 2 + 1;
-    static constexpr int kD = kWPer + kActPer + 1;
+    static constexpr int kD = kWPer + kActPer + 1;  // the most any wavefront issues
     static_assert(kLds <= 160 * 1024, "LDS budget");
     static_assert((kRing - 2) * kD < 64, "vmcnt range");
+    // 16-row tiles: DMA instructions per super-block of wavefront w (the
+    // weights, then a header, activation piece and bsum / d_a load only for
+    // the wavefronts that have one)
+    static constexpr uint32_t kExtra = kQ4K ? 2u : 1u;  // Q4K: bsums (w 0), d_a (w 1); Q6K: d_a (w 0)
+    __host__ __device__ static constexpr int dma_count(uint32_t w) {
+        return (kQ4K ? 4 : 4 + 2) + (w < (uint32_t)kHdrWaves ? (kQ4K ? 1 : 2) : 0) + (w < 4u ? 1 : 0) +
+               (w < kExtra ? 1 : 0);
+    }
 };
 
 // global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
@@ -117,6 +126,22 @@ __device__ __forceinline__ void wait_younger(uint32_t younger) {
     } else {
         if (younger >= (uint32_t)Y) wait_vm<Y * KD>();
         else wait_younger<KD, Y - 1>(younger);
+    }
+}
+
+// wait_younger for a wavefront-uniform per-super-block DMA count kd (one of
+// the few values KLay::dma_count takes)
+template <int Y>
+__device__ __forceinline__ void wait_younger_n(uint32_t kd, uint32_t younger) {
+    switch (kd) {
+    case 4: wait_younger<4, Y>(younger); break;
+    case 5: wait_younger<5, Y>(younger); break;
+    case 6: wait_younger<6, Y>(younger); break;
+    case 7: wait_younger<7, Y>(younger); break;
+    case 8: wait_younger<8, Y>(younger); break;
+    case 9: wait_younger<9, Y>(younger); break;
+    case 10: wait_younger<10, Y>(younger); break;
+    default: wait_vm<0>(); break;
     }
 }
 
@@ -168,7 +193,7 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
     uint4 hdr[2];
 #pragma unroll
     for (int ct = 0; ct < 2; ct++)
-        hdr[ct] = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 64 + ct * 16 + li) * 16);
+        hdr[ct] = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 32 + ct * 16 + li) * 16);
     v4i hi[2], lo[2];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
@@ -237,7 +262,7 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
         if (kQ4K) {
             dw = f16_bits_to_f32(hdr[ct].x & 0xffffu);
         } else {
-            const uint32_t dd = reinterpret_cast<const uint32_t*>(S + L::kWd)[wave * 64 + ct * 16 + li];
+            const uint32_t dd = reinterpret_cast<const uint32_t*>(S + L::kWd)[wave * 32 + ct * 16 + li];
             dw = f16_bits_to_f32(odd_sb ? (dd >> 16) : (dd & 0xffffu));
         }
 #pragma unroll
@@ -316,7 +341,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
         oq[j] = min(col0 + cl, cmax) * w.q_row + ((lane & 7) ^ (cl & 7)) * 16;
     }
     // block header (Q4K) / scales (Q6K) of column lane & 31; Q6K d dword
-    const uint32_t ocol = min(col0 + wave * 32 + lrow, cmax);
+    // (16-row tiles: column 64 * wave + lane, for the first kCols / 64 wavefronts)
+    const uint32_t ocol = min(col0 + (L::kNarrow ? wave * 64 + lane : wave * 32 + lrow), cmax);
     const uint32_t os = ocol * w.s_row, od = ocol * w.d_row;
     // Q6K high-bit words: instruction j covers columns 32*wave + 16j .. +15,
     // lane = 4 * column + slot, slot s holding chunk pair s ^ (column & 3)
@@ -348,14 +374,15 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
         const uint32_t slot = lbase + (i % kRing) * L::kSlot;
 #pragma unroll
         for (int j = 0; j < 4; j++) dma16(w.q + sb * 128, oq[j], slot + L::kWq + (wave * 32 + 8 * j) * 128);
-        dma16(w.s + sb * 16, os, slot + L::kHdr + wave * 64 * 16);
+        if (!L::kNarrow || wave < (uint32_t)L::kHdrWaves) dma16(w.s + sb * 16, os, slot + L::kHdr + wave * 64 * 16);
         if (!kQ4K) {
 #pragma unroll
             for (int j = 0; j < 2; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + (wave * 32 + 16 * j) * 64);
-            dma4(w.d + (sb & ~1u) * 2, od, slot + L::kWd + wave * 64 * 4);
+            if (!L::kNarrow || wave < (uint32_t)L::kHdrWaves)
+                dma4(w.d + (sb & ~1u) * 2, od, slot + L::kWd + wave * 64 * 4);
         }
         if (MT == 0) {
-            dma16(a.img + sb * 128, oa[0], slot + (wave < 4 ? L::kAct + wave * 1024 : L::kDummyAct));
+            if (wave < 4) dma16(a.img + sb * 128, oa[0], slot + L::kAct + wave * 1024);
         } else {
 #pragma unroll
             for (int j = 0; j < L::kActPer; j++) {
@@ -367,9 +394,10 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
         }
         if (wave < kExtraBs) dma16(a.img + sb * 32, obs, slot + L::kBs + wave * 32 * 32);
         else if (wave == kExtraBs) dma4(a.img + sb * 4, oda, slot + L::kDa);
-        else dma4(a.img + sb * 4, oda, slot + L::kDummy);
+        else if (!L::kNarrow) dma4(a.img + sb * 4, oda, slot + L::kDummy);
     };
 
+    const uint32_t kDw = L::dma_count(wave);  // 16-row tiles: this wavefront's DMA per super-block
     constexpr int kAccT = MT == 0 ? 1 : MT;
     v16f acc[kAccT];
 #pragma unroll
@@ -384,7 +412,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     for (uint32_t i = 0; i < nsb; i++) {
         // wait for super-block i: the younger ones in flight are i+1 .. i+kRing-2
         const uint32_t younger = min((uint32_t)(kRing - 2), nsb - 1 - i);
-        wait_younger<kD, kRing - 2>(younger);
+        if constexpr (L::kNarrow) wait_younger_n<kRing - 2>(kDw, younger);
+        else wait_younger<kD, kRing - 2>(younger);
         __syncthreads();  // every wavefront's DMA of i landed; slot (i-1) % kRing is free
         if (i + kRing - 1 < nsb) issue(i + kRing - 1);
 
