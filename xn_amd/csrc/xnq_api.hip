@@ -93,8 +93,9 @@ xnq_status check_weight(uint32_t dtype, size_t n, size_t k) {
         return fail(XNQ_ERR_INVALID,
                     "quantized tensor must have their last dim divisible by block size [%zu, %zu] %zu",
                     n, k, bs);
-    // kernels address every plane with 32-bit byte offsets
-    if (n > 0xffffffffull || k > 0x7fffffffull || n * (k / bs) * type_size(dtype) >= (1ull << 32))
+    // kernels address every plane with 32-bit byte offsets (Q4K / Q6K planes
+    // pad the rows to a multiple of 128)
+    if (n > 0xffffffffull || k > 0x7fffffffull || (n + 127) / 128 * 128 * (k / bs) * type_size(dtype) >= (1ull << 32))
         return fail(XNQ_ERR_INVALID, "tensor too large for the device layout [%zu, %zu]", n, k);
     return XNQ_OK;
 }
@@ -190,15 +191,22 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
         }
         L.q_row = L.nb * raw_stride(dtype);
     }
+    // Q4K / Q6K: q, h and s planes in 128-row tiles (rows padded)
+    const size_t tiled_rows = (dtype == XNQ_Q4K || dtype == XNQ_Q6K) ? (n + kTileRows - 1) / kTileRows * kTileRows : n;
     size_t off = 0;
     L.off_q = off;
-    off = align_up(off + L.q_row * n);
+    off = align_up(off + L.q_row * tiled_rows);
     L.off_h = off;
-    off = align_up(off + L.h_row * n);
+    off = align_up(off + L.h_row * tiled_rows);
     L.off_s = off;
-    off = align_up(off + L.s_row * n);
+    off = align_up(off + L.s_row * tiled_rows);
     L.off_d = off;
     off = align_up(off + L.d_row * n);
+    L.off_st = L.off_s;
+    if (dtype == XNQ_Q4K || dtype == XNQ_Q6K) {
+        L.off_st = off;
+        off = align_up(off + L.s_row * tiled_rows);
+    }
     L.bytes = off;
     *out = L;
     return true;

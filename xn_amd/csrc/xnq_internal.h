@@ -35,12 +35,30 @@ inline size_t align_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a
 //         h plane [n][nb][8][8]  high 2 bits: dword u, byte p, bits 2g'..2g'+1
 //                                hold element 4*(4u+g')+p of the chunk
 //         s plane [n][nb][16] int8 scales, d plane [n][nb] f16
+//   Q4K and Q6K store their q and h planes in 128-row tiles instead of
+//         row after row: super-block sb of rows 128t .. 128t+127 is one
+//         contiguous run of 128 * P bytes (P = the plane's bytes per row and
+//         super-block: q 128, h 64), row r's P bytes at (r & 127) * P in it
+//         (kq_tile_off); rows are padded to a multiple of 128.  A workgroup
+//         that streams a super-block of 128 or 256 consecutive rows then
+//         reads whole contiguous runs.  The s plane is kept twice: [n][nb]
+//         for the matvec kernels (whose per-chunk header loads then touch one
+//         cache line per row) and tiled (st) for the matrix-core kernels,
+//         whose header fetch otherwise reads one line per column.  The d
+//         plane stays [n][nb].
 //   Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K: one q plane [n][nb][stride] of the GGUF
 //         blocks padded to a 4-byte multiple (raw_stride below) so every field
 //         is dword aligned: Q5_0 {d, 2 pad, qh[4], qs[16]}, Q3K 2 tail bytes;
 //         the others are their GGUF bytes unchanged.
 // nb = blocks per row (k/32 for the 32-element types, k/256 for the K types).
 // ---------------------------------------------------------------------------
+
+// Byte offset of (row, super-block sb) in a tiled Q4K / Q6K plane of P bytes
+// per row and super-block (every plane is < 4 GiB, checked at upload).
+__host__ __device__ inline uint32_t kq_tile_off(uint32_t nb, uint32_t row, uint32_t sb, uint32_t P) {
+    return ((row >> 7) * nb + sb) * (P * 128u) + (row & 127u) * P;
+}
+constexpr uint32_t kTileRows = 128;
 
 // Super-block (256-element) types, whose activations are Q8K.
 __host__ __device__ constexpr bool is_kquant(uint32_t dt) {
@@ -59,6 +77,7 @@ struct WLayout {
     size_t n = 0, k = 0, nb = 0;
     size_t q_row = 0, h_row = 0, s_row = 0, d_row = 0;  // bytes per row, per plane
     size_t off_q = 0, off_h = 0, off_s = 0, off_d = 0;  // plane offsets in the allocation
+    size_t off_st = 0;  // Q4K / Q6K: the s plane again, tiled
     size_t bytes = 0;
 };
 
@@ -68,6 +87,7 @@ struct WView {
     const uint8_t* h;
     const uint8_t* s;
     const uint8_t* d;
+    const uint8_t* st;  // Q4K / Q6K: tiled copy of the s plane
     uint32_t q_row, h_row, s_row, d_row;
     uint32_t n, k, nb;
     uint32_t dtype;
@@ -166,6 +186,7 @@ inline WView make_wview(const WLayout& L, const void* base) {
     v.h = b + L.off_h;
     v.s = b + L.off_s;
     v.d = b + L.off_d;
+    v.st = b + L.off_st;
     v.q_row = (uint32_t)L.q_row;
     v.h_row = (uint32_t)L.h_row;
     v.s_row = (uint32_t)L.s_row;
