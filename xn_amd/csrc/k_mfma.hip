@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         const uint8_t* wq = w.q + kq_tile_off(w.nb, n0, sb0, 128);
         const uint8_t* wh = w.h + kq_tile_off(w.nb, n0, sb0, 64);
         const uint8_t* ws = w.st + kq_tile_off(w.nb, n0, sb0, 16);
-        const uint8_t* wd = w.d + (size_t)n0 * w.d_row;
+        const uint8_t* wd = w.dt + kq_tile_off((w.nb + 1) / 2, n0, 0, 4);
         const uint32_t nstage = 4 * nsb;
 
         // DMA instruction p of stage st (parts past kBase only at a super-block's first stage)
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                     dma16(wh + (st >> 2) * 8192 + (st & 3) * 16, lc * 64, raw + L::kQSlot);
                 if (p == kBase) dma16(ws + sb * 2048, lc * 16, epi + L::kEHdr + cw * 64 * 16);
                 if (!kQ4K && p == kBase + 1)
-                    dma4(wd + ((sb0 + sb) & ~1u) * 2, min(col, col_max) * w.d_row, epi + L::kEB + cw * 64 * 4);
+                    dma4(wd + ((sb0 + sb) >> 1) * 512, lc * 4, epi + L::kEB + cw * 64 * 4);
             } else {
                 if (p == kBase)
                     dma4(t_d + ((size_t)rblk(gw) * nsb_all + sb) * 256, lane4, epi + L::kEDa + 64 * gw * 4);

@@ -38,7 +38,8 @@ __device__ __forceinline__ uint32_t q4k_canon(const uint8_t* qs, int E) {
 // for Q4K / Q6K.
 __global__ void repack_kernel(WView w, const uint8_t* __restrict__ src, uint8_t* __restrict__ q,
                               uint8_t* __restrict__ h, uint8_t* __restrict__ s,
-                              uint8_t* __restrict__ d, uint8_t* __restrict__ st, size_t total) {
+                              uint8_t* __restrict__ d, uint8_t* __restrict__ st, uint8_t* __restrict__ dt,
+                              size_t total) {
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= total) return;
     if (w.dtype == XNQ_Q8_0 || w.dtype == XNQ_Q4_0) {
@@ -108,6 +109,9 @@ __global__ void repack_kernel(WView w, const uint8_t* __restrict__ src, uint8_t*
         uint8_t* dp = d + row * w.d_row + sb * 2;
         dp[0] = blk[208];
         dp[1] = blk[209];
+        uint8_t* dtp = dt + kq_tile_off((w.nb + 1) / 2, (uint32_t)row, (uint32_t)(sb >> 1), 4) + (sb & 1) * 2;
+        dtp[0] = blk[208];
+        dtp[1] = blk[209];
     }
 }
 
@@ -357,7 +361,7 @@ hipError_t launch_repack(const WLayout& L, const void* gguf_dev, void* dst_dev, 
     if (total == 0) return hipSuccess;
     repack_kernel<<<blocks_for(total, 256), 256, 0, s>>>(
         w, static_cast<const uint8_t*>(gguf_dev), base + L.off_q, base + L.off_h, base + L.off_s,
-        base + L.off_d, base + L.off_st, total);
+        base + L.off_d, base + L.off_st, base + L.off_dt, total);
     return hipGetLastError();
 }
 

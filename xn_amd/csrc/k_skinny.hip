@@ -344,7 +344,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     // block header (Q4K) / scales (Q6K) of column lane & 31; Q6K d dword
     // (16-row tiles: column 64 * wave + lane, for the first kCols / 64 wavefronts)
     const uint32_t ocol = min(col0 + (L::kNarrow ? wave * 64 + lane : wave * 32 + lrow), cmax);
-    const uint32_t os = kq_tile_off(w.nb, ocol, 0, 16), od = ocol * w.d_row;  // tiled s copy
+    // tiled copies of the s and (Q6K) d planes
+    const uint32_t os = kq_tile_off(w.nb, ocol, 0, 16), od = kq_tile_off((w.nb + 1) / 2, ocol, 0, 4);
     // Q6K high-bit words: instruction j covers columns 32*wave + 16j .. +15,
     // lane = 4 * column + slot, slot s holding chunk pair s ^ (column & 3)
     uint32_t oh[2];
@@ -381,7 +382,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 #pragma unroll
             for (int j = 0; j < 2; j++) dma16(w.h + sb * 64 * 128, oh[j], slot + L::kWh + (wave * 32 + 16 * j) * 64);
             if (!L::kNarrow || wave < (uint32_t)L::kHdrWaves)
-                dma4(w.d + (sb & ~1u) * 2, od, slot + L::kWd + wave * 64 * 4);
+                dma4(w.dt + (sb >> 1) * 512, od, slot + L::kWd + wave * 64 * 4);
         }
         if (MT == 0) {
             if (wave < 4) dma16(a.img + sb * 128, oa[0], slot + L::kAct + wave * 1024);

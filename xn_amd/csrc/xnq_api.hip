@@ -203,9 +203,14 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
     L.off_d = off;
     off = align_up(off + L.d_row * n);
     L.off_st = L.off_s;
+    L.off_dt = L.off_d;
     if (dtype == XNQ_Q4K || dtype == XNQ_Q6K) {
         L.off_st = off;
         off = align_up(off + L.s_row * tiled_rows);
+    }
+    if (dtype == XNQ_Q6K) {
+        L.off_dt = off;
+        off = align_up(off + L.d_row * tiled_rows);
     }
     L.bytes = off;
     *out = L;

@@ -44,8 +44,9 @@ inline size_t align_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a
 //         reads whole contiguous runs.  The s plane is kept twice: [n][nb]
 //         for the matvec kernels (whose per-chunk header loads then touch one
 //         cache line per row) and tiled (st) for the matrix-core kernels,
-//         whose header fetch otherwise reads one line per column.  The d
-//         plane stays [n][nb].
+//         whose header fetch otherwise reads one line per column.  Q6K's d
+//         plane likewise: [n][nb] f16, and tiled (dt) with P = 4 bytes per
+//         super-block pair.
 //   Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K: one q plane [n][nb][stride] of the GGUF
 //         blocks padded to a 4-byte multiple (raw_stride below) so every field
 //         is dword aligned: Q5_0 {d, 2 pad, qh[4], qs[16]}, Q3K 2 tail bytes;
@@ -78,6 +79,7 @@ struct WLayout {
     size_t q_row = 0, h_row = 0, s_row = 0, d_row = 0;  // bytes per row, per plane
     size_t off_q = 0, off_h = 0, off_s = 0, off_d = 0;  // plane offsets in the allocation
     size_t off_st = 0;  // Q4K / Q6K: the s plane again, tiled
+    size_t off_dt = 0;  // Q6K: the d plane again, tiled by super-block pairs
     size_t bytes = 0;
 };
 
@@ -88,6 +90,7 @@ struct WView {
     const uint8_t* s;
     const uint8_t* d;
     const uint8_t* st;  // Q4K / Q6K: tiled copy of the s plane
+    const uint8_t* dt;  // Q6K: tiled copy of the d plane (4 bytes = a super-block pair)
     uint32_t q_row, h_row, s_row, d_row;
     uint32_t n, k, nb;
     uint32_t dtype;
@@ -187,6 +190,7 @@ inline WView make_wview(const WLayout& L, const void* base) {
     v.s = b + L.off_s;
     v.d = b + L.off_d;
     v.st = b + L.off_st;
+    v.dt = b + L.off_dt;
     v.q_row = (uint32_t)L.q_row;
     v.h_row = (uint32_t)L.h_row;
     v.s_row = (uint32_t)L.s_row;
