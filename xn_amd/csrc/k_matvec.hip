@@ -41,13 +41,13 @@ __global__ void block_ints_kernel(WView w, AView a, uint32_t m, int32_t* __restr
             const uint4 meta = *reinterpret_cast<const uint4*>(w.s + (size_t)row * w.s_row + (size_t)b * 16);
             int sc, mn, lo, hi;
             q4k_scale_min(meta.y, meta.z, meta.w, (int)(c & 7), sc, mn);
-            nib_dot2(*reinterpret_cast<const uint4*>(w.q + kq_tile_off(w.nb, row, c >> 3, 128) + (c & 7) * 16), av, lo,
+            nib_dot2(*reinterpret_cast<const uint4*>(w.q + (size_t)row * w.q_row + (size_t)c * 16), av, lo,
                      hi);
             r0 += sc * (lo + hi);
             r1 += mn * ((int)(int16_t)(sv & 0xffff) + (int)(int16_t)(sv >> 16));
         } else {
-            const uint4 ql = *reinterpret_cast<const uint4*>(w.q + kq_tile_off(w.nb, row, c >> 3, 128) + (c & 7) * 16);
-            const uint2 qh = *reinterpret_cast<const uint2*>(w.h + kq_tile_off(w.nb, row, c >> 3, 64) + (c & 7) * 8);
+            const uint4 ql = *reinterpret_cast<const uint4*>(w.q + (size_t)row * w.q_row + (size_t)c * 16);
+            const uint2 qh = *reinterpret_cast<const uint2*>(w.h + (size_t)row * w.h_row + (size_t)c * 8);
             const int8_t* sc = reinterpret_cast<const int8_t*>(w.s + (size_t)row * w.s_row + (size_t)b * 16);
             const uint32_t j = c & 7;
             r0 += q6k_chunk_int(ql, qh, av, sc[2 * j], sc[2 * j + 1], (int)(int16_t)(sv & 0xffff),

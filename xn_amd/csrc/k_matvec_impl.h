@@ -179,13 +179,12 @@ __device__ __forceinline__ void load_chunk(const WView& w, uint32_t row, uint32_
         ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
         ch.dw = f16_bits_to_f32(ldw(reinterpret_cast<const uint16_t*>(w.d + (row * w.d_row + c * 2))));
     } else if (DT == XNQ_Q4K) {
-        // tiled q plane (kq_tile_off), row-major s plane
-        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (kq_tile_off(w.nb, row, c >> 3, 128) + (c & 7) * 16)));
+        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
         ch.x = ldw(reinterpret_cast<const uint4*>(w.s + (row * w.s_row + (c >> 3) * 16)));
     } else if (DT == XNQ_Q6K) {
         const uint32_t sb = c >> 3, j = c & 7;
-        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (kq_tile_off(w.nb, row, sb, 128) + j * 16)));
-        const uint2 h = ldw(reinterpret_cast<const uint2*>(w.h + (kq_tile_off(w.nb, row, sb, 64) + j * 8)));
+        ch.q = ldw(reinterpret_cast<const uint4*>(w.q + (row * w.q_row + c * 16)));
+        const uint2 h = ldw(reinterpret_cast<const uint2*>(w.h + (row * w.h_row + c * 8)));
         ch.x.x = h.x;
         ch.x.y = h.y;
         ch.x.z = ldw(reinterpret_cast<const uint16_t*>(w.s + (row * w.s_row + sb * 16 + 2 * j)));

@@ -332,12 +332,13 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         const uint32_t gw = wave & 3;                  // index within the group
         const uint32_t bc = gw >> 1, cw = gw & 1;      // group 0: chunk and 64-column half
         const uint32_t col = cw * 64 + lane;           // group 0: this lane's weight column
-        // tiled q, h and st planes (kq_tile_off): the 128-column tile starting
-        // at n0, super-block sb0 + sb at sb * 128 * P, this lane's column at
-        // col * P
+        // q and h planes row-major; the tiled header copy (kq_tile_off): the
+        // 128-column tile starting at n0, super-block sb0 + sb at sb * 2048,
+        // this lane's column at col * 16
         const uint32_t lc = min(col, col_max);
-        const uint8_t* wq = w.q + kq_tile_off(w.nb, n0, sb0, 128);
-        const uint8_t* wh = w.h + kq_tile_off(w.nb, n0, sb0, 64);
+        const uint32_t q_lane = lc * w.q_row;
+        const uint8_t* wq = w.q + (size_t)n0 * w.q_row + sb0 * 128;
+        const uint8_t* wh = w.h + (size_t)n0 * w.h_row + sb0 * 64;
         const uint8_t* ws = w.st + kq_tile_off(w.nb, n0, sb0, 16);
         const uint8_t* wd = w.dt + kq_tile_off((w.nb + 1) / 2, n0, 0, 4);
         const uint32_t nstage = 4 * nsb;
@@ -356,9 +357,8 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
             if (G == 0) {
                 const uint32_t raw = lbase + L::kOffRaw + slot * L::kRawSlot + (bc * kBN + cw * 64) * 16;
                 // chunk 2 * (st & 3) + bc of super-block st >> 2
-                if (p == 2) dma16(wq + (st >> 2) * 16384 + ((st & 3) * 2 + bc) * 16, lc * 128, raw);
-                if (!kQ4K && p == 3)  // qh of chunks 2st, 2st+1
-                    dma16(wh + (st >> 2) * 8192 + (st & 3) * 16, lc * 64, raw + L::kQSlot);
+                if (p == 2) dma16(wq + bc * 16 + st * 32, q_lane, raw);
+                if (!kQ4K && p == 3) dma16(wh + st * 16, q_lane >> 1, raw + L::kQSlot);  // qh of chunks 2st, 2st+1
                 if (p == kBase) dma16(ws + sb * 2048, lc * 16, epi + L::kEHdr + cw * 64 * 16);
                 if (!kQ4K && p == kBase + 1)
                     dma4(wd + ((sb0 + sb) >> 1) * 512, lc * 4, epi + L::kEB + cw * 64 * 4);

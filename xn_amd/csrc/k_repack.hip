@@ -69,7 +69,7 @@ __global__ void repack_kernel(WView w, const uint8_t* __restrict__ src, uint8_t*
             }
             out[dw] = v;
         }
-        *reinterpret_cast<uint4*>(q + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)sb, 128) + c * 16) =
+        *reinterpret_cast<uint4*>(q + row * w.q_row + sb * 128 + c * 16) =
             make_uint4(out[0], out[1], out[2], out[3]);
         if (c == 0) {
             uint8_t* so = s + row * w.s_row + sb * 16;
@@ -99,9 +99,9 @@ __global__ void repack_kernel(WView w, const uint8_t* __restrict__ src, uint8_t*
             hi2[g >> 2] |= v << (8 * p + 2 * (g & 3));
         }
     }
-    *reinterpret_cast<uint4*>(q + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)sb, 128) + c * 16) =
+    *reinterpret_cast<uint4*>(q + row * w.q_row + sb * 128 + c * 16) =
         make_uint4(lo4[0], lo4[1], lo4[2], lo4[3]);
-    *reinterpret_cast<uint2*>(h + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)sb, 64) + c * 8) = make_uint2(hi2[0], hi2[1]);
+    *reinterpret_cast<uint2*>(h + row * w.h_row + sb * 64 + c * 8) = make_uint2(hi2[0], hi2[1]);
     if (c == 0) {
         uint8_t* so = s + row * w.s_row + sb * 16;
         uint8_t* sto = st + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)sb, 16);
@@ -142,7 +142,7 @@ __global__ void unrepack_kernel(WView w, uint8_t* __restrict__ dst, size_t total
         for (size_t i = 0; i < qb; i++) o[2 + i] = qi[i];
         return;
     }
-    const uint8_t* qrow = w.q + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)b, 128);
+    const uint8_t* qrow = w.q + row * w.q_row + b * 128;
     if (w.dtype == XNQ_Q4K) {
         uint8_t* o = dst + t * 144;
         const uint8_t* si = w.s + row * w.s_row + b * 16;
@@ -157,7 +157,7 @@ __global__ void unrepack_kernel(WView w, uint8_t* __restrict__ dst, size_t total
         return;
     }
     uint8_t* o = dst + t * 210;
-    const uint8_t* hrow = w.h + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)b, 64);
+    const uint8_t* hrow = w.h + row * w.h_row + b * 64;
     for (int hh = 0; hh < 2; hh++)
         for (int l = 0; l < 32; l++) {
             uint32_t v[4];
@@ -197,7 +197,7 @@ __global__ void dequant_kernel(WView w, float* __restrict__ y, size_t total) {
         return;
     }
     const size_t sb = c / 8, j = c % 8;
-    const uint8_t* qi = w.q + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)sb, 128) + j * 16;
+    const uint8_t* qi = w.q + row * w.q_row + sb * 128 + j * 16;
     if (w.dtype == XNQ_Q4K) {  // k_quants.rs:1475-1503
         const uint8_t* si = w.s + row * w.s_row + sb * 16;
         const float d = f16_bits_to_f32(ld16(si)), mn = f16_bits_to_f32(ld16(si + 2));
@@ -209,7 +209,7 @@ __global__ void dequant_kernel(WView w, float* __restrict__ y, size_t total) {
         return;
     }
     // Q6K, k_quants.rs:1874-1904
-    const uint8_t* hi = w.h + kq_tile_off(w.nb, (uint32_t)row, (uint32_t)sb, 64) + j * 8;
+    const uint8_t* hi = w.h + row * w.h_row + sb * 64 + j * 8;
     const int8_t* sc = reinterpret_cast<const int8_t*>(w.s + row * w.s_row + sb * 16);
     const float d = f16_bits_to_f32(ld16(w.d + row * w.d_row + sb * 2));
     for (int e = 0; e < 32; e++) {

@@ -332,14 +332,14 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     // ---- the DMA of super-block i: kD instructions per wavefront ----
     // Per-lane byte offsets are fixed for the whole walk; the super-block
     // moves only the uniform base pointers (one super-block of a 128-row
-    // tile is 128 * P bytes in the tiled q, h and st planes).
+    // tile is 128 * P bytes in the tiled st and dt copies).
     // weight chunks: instruction j covers columns 32*wave + 8j .. +7,
     // lane = 8 * column + slot, slot s holding chunk s ^ (column & 7)
     uint32_t oq[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const uint32_t cl = wave * 32 + 8 * j + (lane >> 3);
-        oq[j] = kq_tile_off(w.nb, min(col0 + cl, cmax), 0, 128) + ((lane & 7) ^ (cl & 7)) * 16;
+        oq[j] = min(col0 + cl, cmax) * w.q_row + ((lane & 7) ^ (cl & 7)) * 16;
     }
     // block header (Q4K) / scales (Q6K) of column lane & 31; Q6K d dword
     // (16-row tiles: column 64 * wave + lane, for the first kCols / 64 wavefronts)
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const uint32_t cl = wave * 32 + 16 * j + (lane >> 2);
-        oh[j] = kQ4K ? 0u : kq_tile_off(w.nb, min(col0 + cl, cmax), 0, 64) + ((lane & 3) ^ (cl & 3)) * 16;
+        oh[j] = kQ4K ? 0u : min(col0 + cl, cmax) * w.h_row + ((lane & 3) ^ (cl & 3)) * 16;
     }
     // activation pieces of 1 KiB.  MT == 1: piece = chunk c, lanes 0-31 rows
     // of half 0, lanes 32-63 rows of half 1.  MT == 2: piece = (chunk, half),
@@ -375,12 +375,12 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
         const uint32_t sb = sb0 + i;
         const uint32_t slot = lbase + (i % kRing) * L::kSlot;
 #pragma unroll
-        for (int j = 0; j < 4; j++) dma16(w.q + sb * 128 * 128, oq[j], slot + L::kWq + (wave * 32 + 8 * j) * 128);
+        for (int j = 0; j < 4; j++) dma16(w.q + sb * 128, oq[j], slot + L::kWq + (wave * 32 + 8 * j) * 128);
         if (!L::kNarrow || wave < (uint32_t)L::kHdrWaves)
             dma16(w.st + sb * 16 * 128, os, slot + L::kHdr + wave * 64 * 16);
         if (!kQ4K) {
 #pragma unroll
-            for (int j = 0; j < 2; j++) dma16(w.h + sb * 64 * 128, oh[j], slot + L::kWh + (wave * 32 + 16 * j) * 64);
+            for (int j = 0; j < 2; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + (wave * 32 + 16 * j) * 64);
             if (!L::kNarrow || wave < (uint32_t)L::kHdrWaves)
                 dma4(w.dt + (sb >> 1) * 512, od, slot + L::kWd + wave * 64 * 4);
         }

@@ -191,15 +191,15 @@ bool weight_layout(uint32_t dtype, size_t n, size_t k, WLayout* out, std::string
         }
         L.q_row = L.nb * raw_stride(dtype);
     }
-    // Q4K / Q6K: q, h and s planes in 128-row tiles (rows padded)
-    const size_t tiled_rows = (dtype == XNQ_Q4K || dtype == XNQ_Q6K) ? (n + kTileRows - 1) / kTileRows * kTileRows : n;
+    // Q4K / Q6K: the tiled copies pad their rows to a multiple of 128
+    const size_t tiled_rows = (n + kTileRows - 1) / kTileRows * kTileRows;
     size_t off = 0;
     L.off_q = off;
-    off = align_up(off + L.q_row * tiled_rows);
+    off = align_up(off + L.q_row * n);
     L.off_h = off;
-    off = align_up(off + L.h_row * tiled_rows);
+    off = align_up(off + L.h_row * n);
     L.off_s = off;
-    off = align_up(off + L.s_row * tiled_rows);
+    off = align_up(off + L.s_row * n);
     L.off_d = off;
     off = align_up(off + L.d_row * n);
     L.off_st = L.off_s;

@@ -35,18 +35,15 @@ inline size_t align_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a
 //         h plane [n][nb][8][8]  high 2 bits: dword u, byte p, bits 2g'..2g'+1
 //                                hold element 4*(4u+g')+p of the chunk
 //         s plane [n][nb][16] int8 scales, d plane [n][nb] f16
-//   Q4K and Q6K store their q and h planes in 128-row tiles instead of
-//         row after row: super-block sb of rows 128t .. 128t+127 is one
-//         contiguous run of 128 * P bytes (P = the plane's bytes per row and
-//         super-block: q 128, h 64), row r's P bytes at (r & 127) * P in it
-//         (kq_tile_off); rows are padded to a multiple of 128.  A workgroup
-//         that streams a super-block of 128 or 256 consecutive rows then
-//         reads whole contiguous runs.  The s plane is kept twice: [n][nb]
-//         for the matvec kernels (whose per-chunk header loads then touch one
-//         cache line per row) and tiled (st) for the matrix-core kernels,
-//         whose header fetch otherwise reads one line per column.  Q6K's d
-//         plane likewise: [n][nb] f16, and tiled (dt) with P = 4 bytes per
-//         super-block pair.
+//   Q4K and Q6K also keep a second copy of their s plane (st) and Q6K of
+//         its d plane (dt) in 128-row tiles, for the matrix-core kernels:
+//         super-block sb of rows 128t .. 128t+127 is one contiguous run of
+//         128 * P bytes (P = the plane's bytes per row and super-block: s 16,
+//         d 4 per super-block pair), row r's P bytes at (r & 127) * P in it
+//         (kq_tile_off); rows are padded to a multiple of 128.  Their header
+//         fetch covers 64 or 128 consecutive columns, which is one cache line
+//         per column row-major and contiguous tiled; the matvec kernels read
+//         the row-major planes.
 //   Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K: one q plane [n][nb][stride] of the GGUF
 //         blocks padded to a 4-byte multiple (raw_stride below) so every field
 //         is dword aligned: Q5_0 {d, 2 pad, qh[4], qs[16]}, Q3K 2 tail bytes;
