@@ -281,7 +281,7 @@ def sweep(args, dev, stream, gen) -> dict:
             e1.synchronize()
             times.append(e0.elapsed_time(e1) / 5)
         ms = float(np.median(times))
-        rows.append({"config": "5 decode step (DecodeStep: q/k/v grouped, SiLU-gated gate/up, one graph)",
+        rows.append({"config": "5 decode step (DecodeStep: q/k/v grouped, one MLP call per layer, one graph)",
                      "batch": b, "weight_bytes": wtotal,
                      "us_step": round(ms * 1e3, 1), "gbs_weights": round(wtotal / (ms * 1e-3) / 1e9, 1),
                      "frac_hbm": round(wtotal / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})

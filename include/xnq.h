@@ -168,6 +168,18 @@ xnq_status xnq_matmul_t_group(const xnq_qtensor* const* qts, size_t count, size_
                               const float* lhs_dev, float* const* dsts_dev, void* workspace_dev,
                               size_t workspace_bytes, void* stream);
 
+/* The whole SwiGLU MLP of llama.rs:236-264 (Mlp::forward): h[m x f] =
+ * silu(lhs . gate^T) * (lhs . up^T) as silu_gate above, then dst[m x n] =
+ * h . down^T with down of shape (n, f).  Both results are written.  With
+ * gate/up on the small-batch MFMA route and a K-quant down weight, the
+ * gate/up split-sum also quantizes h for the down projection (one launch
+ * fewer); otherwise it is silu_gate followed by matmul_t_ws.  The results are
+ * the bits those two calls produce. */
+size_t xnq_mlp_t_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_qtensor* down, size_t m);
+xnq_status xnq_mlp_t(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_qtensor* down, size_t m, size_t k,
+                     size_t f, const float* lhs_dev, void* workspace_dev, size_t workspace_bytes, float* h_dev,
+                     float* dst_dev, void* stream);
+
 /* The two halves of matmul_t, for callers that keep the quantized
  * activation around or manage the scratch memory themselves
  * (k_quants.rs:2014-2026 quantize_lhs, then T::matmul).  The workspace

@@ -459,3 +459,35 @@ def test_skinny_split_k_back_to_back(orc, dev, dt, m):
         assert_close(outs[i].cpu().numpy(), want, f"call {i} dt={dt} m={m}")
         want_h = _silu(want.astype(np.float64)) * orc.matmul(dt, x, ub, n)
         assert_close(gated[i].cpu().numpy(), want_h, f"gated call {i} dt={dt} m={m}")
+
+
+@pytest.mark.parametrize("dt,down_dt", [(Q4K, Q6K), (Q6K, Q4K), (Q4_0, Q4K)])
+@pytest.mark.parametrize("m", [1, 4, 16, 40, 80])
+def test_mlp_t(orc, dev, dt, down_dt, m):
+    """The SwiGLU MLP entry (llama.rs:236-264): h and y are the bits that
+    silu_gate followed by matmul_t produce (on the small-batch MFMA route the
+    gate/up split-sum also quantizes h for the down projection), and match
+    the oracle."""
+    from xn_amd.quantized import matmul_t_silu_gate, mlp_t
+
+    k, f, n = 2048, 1024, 384
+    rng = np.random.default_rng(8800 + 7 * dt + down_dt + m)
+    gb = orc.from_float(dt, rng.normal(0, 0.02, (f, k)))
+    ub = orc.from_float(dt, rng.normal(0, 0.02, (f, k)))
+    db = orc.from_float(down_dt, rng.normal(0, 0.02, (n, f)))
+    g, u, d = upload(gb, f, k, dt, dev), upload(ub, f, k, dt, dev), upload(db, n, f, down_dt, dev)
+    x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float32)).to(dev)
+    h = torch.empty((m, f), dtype=torch.float32, device=dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    mlp_t(g, u, d, m, x, h, y)
+    h2 = torch.empty_like(h)
+    y2 = torch.empty_like(y)
+    matmul_t_silu_gate(g, u, (m, k, f), x, h2)
+    d.matmul_t((m, f, n), h2, y2)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2), f"h differs from silu_gate, dt={dt} m={m}"
+    assert torch.equal(y, y2), f"y differs from silu_gate + matmul_t, dt={dt} m={m}"
+    xh = x.cpu().numpy()
+    want_h = _silu(orc.matmul(dt, xh, gb, f).astype(np.float64)) * orc.matmul(dt, xh, ub, f)
+    assert_close(h.cpu().numpy(), want_h, f"mlp h dt={dt} m={m}")
+    assert_close(y.cpu().numpy(), orc.matmul(down_dt, h.cpu().numpy(), db, n), f"mlp y dt={dt} m={m}")

@@ -41,6 +41,9 @@ SIGNATURES = {
     "xnq_qtensor_matmul_t_noalloc": (c_int, [c_void, c_size, c_size, c_size, c_void, c_void, c_void]),
     "xnq_matmul_t_silu_gate_workspace_size": (c_size, [c_void, c_void, c_size]),
     "xnq_matmul_t_silu_gate": (c_int, [c_void, c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void]),
+    "xnq_mlp_t_workspace_size": (c_size, [c_void, c_void, c_void, c_size]),
+    "xnq_mlp_t": (c_int, [c_void, c_void, c_void, c_size, c_size, c_size, c_void, c_void, c_size, c_void, c_void,
+                          c_void]),
     "xnq_matmul_t_group_workspace_size": (c_size, [ctypes.POINTER(c_void), c_size, c_size]),
     "xnq_matmul_t_group": (c_int, [ctypes.POINTER(c_void), c_size, c_size, c_size, c_void, ctypes.POINTER(c_void), c_void,
                                    c_size, c_void]),

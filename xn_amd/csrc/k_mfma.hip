@@ -44,6 +44,7 @@
 
 #include "xnq_device.h"
 #include "xnq_internal.h"
+#include "xnq_quant_dev.h"
 
 namespace xnq {
 
@@ -124,7 +125,43 @@ __global__ __launch_bounds__(256) void sum_group_kernel(SumGroup S, uint32_t spl
     S.y[t][i] = sum_over_splits(S.part[t] + i, S.cnt[t], splits);
 }
 
+// The gate/up split-sum with its SiLU-multiply, fused with the Q8K
+// quantization of the result for the next matmul (the down projection):
+// one wavefront per 256-element block of a row of h, four consecutive
+// elements per lane, the same arithmetic as sum_group_kernel (silu) followed
+// by quantize_q8k_kernel, so h and the image are the bits those two write.
+__global__ __launch_bounds__(256) void sum_silu_quant_kernel(SumGroup S, uint32_t splits, uint32_t m, uint32_t n,
+                                                             ActImg A, uint8_t* __restrict__ img) {
+    const uint32_t nbr = n / 256;
+    const size_t blk = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= (size_t)m * nbr) return;  // uniform over the wavefront
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = (uint32_t)(blk / nbr), b = (uint32_t)(blk % nbr);
+    const size_t i0 = (size_t)row * n + (size_t)b * 256 + 4 * lane;
+    float h[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float g = sum_over_splits(S.part[0] + i0 + e, S.cnt[0], splits);
+        const float u = sum_over_splits(S.part[1] + i0 + e, S.cnt[1], splits);
+        h[e] = g / (1.0f + expf(0.0f - g)) * u;
+    }
+    const float4 v = make_float4(h[0], h[1], h[2], h[3]);
+    *reinterpret_cast<float4*>(S.y[0] + i0) = v;
+    const Q8KLane r = q8k_quant_wave(v, lane);
+    q8k_store(img + (size_t)row * A.row_bytes, A, b, lane, r);
+}
+
 }  // namespace
+
+hipError_t launch_sum_silu_quant(const SumGroup& S, uint32_t splits, size_t m, size_t n, const ALayout& L,
+                                 void* img, hipStream_t s) {
+    if (L.act_dtype != XNQ_Q8K || L.tiled || L.k != n || L.m != m || n % 256) return hipErrorInvalidValue;
+    const size_t blocks = m * (n / 256);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(sum_silu_quant_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, s, S, splits,
+                       (uint32_t)m, (uint32_t)n, L.img, static_cast<uint8_t*>(img));
+    return hipGetLastError();
+}
 
 hipError_t launch_sum_group(const SumGroup& S, uint32_t splits, bool silu, hipStream_t s) {
     size_t total = 0;

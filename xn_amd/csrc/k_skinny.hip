@@ -553,7 +553,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 
 template <int DT, int MT, int NW>
 hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
-                            hipStream_t s) {
+                            hipStream_t s, const ALayout* next, void* next_img) {
     using L = KLay<DT, MT, NW>;
     constexpr int kCols = L::kCols;
     {
@@ -585,6 +585,7 @@ hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t 
     hipLaunchKernelGGL((skinny_kernel<DT, MT, NW>), grid, dim3(L::kThreads), L::kLds, s, G, O, a, (uint32_t)m, per);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !reduce) return e;
+    if (silu && next) return launch_sum_silu_quant(S, splits, m, G.w[0].n, *next, next_img, s);
     return launch_sum_group(S, splits, silu, s);
 }
 
@@ -633,7 +634,7 @@ bool skinny_supported(uint32_t dtype, size_t m, size_t n, size_t k) {
 }
 
 hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
-                               hipStream_t s) {
+                               hipStream_t s, const ALayout* next, void* next_img) {
     if (m == 0 || G.count == 0) return hipSuccess;
     if (m > 64 || G.count > (uint32_t)kMaxGroup || (silu && G.count != 2)) return hipErrorInvalidValue;
     if (silu && !partial) return hipErrorInvalidValue;
@@ -644,13 +645,13 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
 #define XNQ_SK(DT)                                                                                   \
     if (G.w[0].dtype == DT) {                                                                        \
         if (m <= 16 && skinny16())                                                                 \
-            return w8 ? launch_skinny_dt<DT, 0, 8>(G, a, m, splits, partial, silu, s)               \
-                      : launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s);              \
+            return w8 ? launch_skinny_dt<DT, 0, 8>(G, a, m, splits, partial, silu, s, next, next_img)               \
+                      : launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s, next, next_img);              \
         if (m <= 32)                                                                                 \
-            return w8 ? launch_skinny_dt<DT, 1, 8>(G, a, m, splits, partial, silu, s)               \
-                      : launch_skinny_dt<DT, 1, 4>(G, a, m, splits, partial, silu, s);              \
-        return w8 ? launch_skinny_dt<DT, 2, 8>(G, a, m, splits, partial, silu, s)                   \
-                  : launch_skinny_dt<DT, 2, 4>(G, a, m, splits, partial, silu, s);                  \
+            return w8 ? launch_skinny_dt<DT, 1, 8>(G, a, m, splits, partial, silu, s, next, next_img)               \
+                      : launch_skinny_dt<DT, 1, 4>(G, a, m, splits, partial, silu, s, next, next_img);              \
+        return w8 ? launch_skinny_dt<DT, 2, 8>(G, a, m, splits, partial, silu, s, next, next_img)                   \
+                  : launch_skinny_dt<DT, 2, 4>(G, a, m, splits, partial, silu, s, next, next_img);                  \
     }
     XNQ_SK(XNQ_Q4K)
     XNQ_SK(XNQ_Q6K)

@@ -728,7 +728,8 @@ static size_t skinny_group_ws(const xnq_qtensor* const* qts, size_t count, size_
 // into G.y[0]).
 static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
                                    const float* lhs_dev, float* const* dsts, void* workspace_dev,
-                                   size_t workspace_bytes, bool silu, void* stream, int forced);
+                                   size_t workspace_bytes, bool silu, void* stream, int forced,
+                                   const ALayout* next = nullptr, void* next_img = nullptr);
 
 static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* const* dsts) {
     WGroup g{};
@@ -746,7 +747,8 @@ static WGroup make_group(const xnq_qtensor* const* qts, size_t count, float* con
 
 static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, size_t k,
                                    const float* lhs_dev, float* const* dsts, void* workspace_dev,
-                                   size_t workspace_bytes, bool silu, void* stream, int forced) {
+                                   size_t workspace_bytes, bool silu, void* stream, int forced,
+                                   const ALayout* next, void* next_img) {
     const uint32_t dt = qts[0]->L.dtype;
     const size_t need = skinny_group_ws(qts, count, m, forced);
     if (!workspace_dev || workspace_bytes < need)
@@ -759,7 +761,7 @@ static xnq_status run_skinny_group(const xnq_qtensor* const* qts, size_t count, 
     const AView a = make_aview(act_layout(dt, m, k, forced), workspace_dev);
     float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace_dev) + partial_offset(dt, m, k, forced));
     const hipError_t e = launch_skinny_group(G, a, m, skinny_splits(m, joined_n(qts, count), k), partial, silu,
-                                             (hipStream_t)stream);
+                                             (hipStream_t)stream, next, next_img);
     if (e != hipSuccess) return hip_fail(e, "grouped skinny kernel");
     return XNQ_OK;
 }
@@ -831,6 +833,67 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     const hipError_t e = launch_silu_mul(dst_dev, u, m * n, s);
     if (e != hipSuccess) return hip_fail(e, "silu_mul kernel");
     return XNQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The SwiGLU MLP of llama.rs:236-264: h = silu(x . gate^T) * (x . up^T),
+// y = h . down^T.  With gate/up on the small-batch MFMA route and a K-quant
+// down weight, the gate/up split-sum also writes the down projection's
+// activation image (one launch fewer than silu_gate + matmul_t); otherwise
+// it is exactly those two calls.  The workspace holds both calls' scratch.
+
+static bool mlp_fused(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_qtensor* down, size_t m,
+                      int forced) {
+    const xnq_qtensor* pair[2] = {gate, up};
+    if (gate->L.n != up->L.n || !skinny_group(pair, 2, m, forced)) return false;
+    if (down->device != gate->device || !is_kquant(down->L.dtype) || fused_route(down, m, forced)) return false;
+    const ALayout L = act_layout(down->L.dtype, m, down->L.k, forced);
+    return L.act_dtype == XNQ_Q8K && !L.tiled && down->L.k % 256 == 0;
+}
+
+static size_t mlp_ws_impl(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_qtensor* down, size_t m,
+                          int forced) {
+    if (!gate || !up || !down) return 0;
+    const size_t a = silu_gate_ws_impl(gate, up, m, forced), b = matmul_t_workspace_size_impl(down, m, forced);
+    return b ? align_up(a, kAlign) + b : a;
+}
+
+size_t xnq_mlp_t_workspace_size(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_qtensor* down, size_t m) {
+    return mlp_ws_impl(gate, up, down, m, g_route.load());
+}
+
+xnq_status xnq_mlp_t(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_qtensor* down, size_t m, size_t k,
+                     size_t f, const float* lhs_dev, void* workspace_dev, size_t workspace_bytes, float* h_dev,
+                     float* dst_dev, void* stream) {
+    if (!gate || !up || !down) return fail(XNQ_ERR_INVALID, "null qtensor");
+    xnq_status st = check_mkn(gate, m, k, f);
+    if (!st) st = check_mkn(up, m, k, f);
+    if (!st) st = check_mkn(down, m, f, down->L.n);
+    if (st) return st;
+    if (gate->device != up->device || gate->device != down->device)
+        return fail(XNQ_ERR_INVALID, "gate, up and down live on different devices");
+    if (m == 0) return XNQ_OK;
+    if (!lhs_dev || !h_dev || !dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
+    const int forced = g_route.load();
+    const size_t need = mlp_ws_impl(gate, up, down, m, forced);
+    if (need && (!workspace_dev || workspace_bytes < need))
+        return fail(XNQ_ERR_INVALID, "workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
+    const size_t a = silu_gate_ws_impl(gate, up, m, forced);
+    const size_t off_b = align_up(a, kAlign);
+    uint8_t* wsb = need > a ? static_cast<uint8_t*>(workspace_dev) + off_b : nullptr;
+    const size_t bytes_b = need > a ? need - off_b : 0;
+    if (mlp_fused(gate, up, down, m, forced)) {
+        const xnq_qtensor* pair[2] = {gate, up};
+        float* dsts[2] = {h_dev, nullptr};
+        const ALayout Ld = act_layout(down->L.dtype, m, f, forced);
+        st = check_lhs(gate->L.dtype, k);
+        if (!st) st = run_skinny_group(pair, 2, m, k, lhs_dev, dsts, workspace_dev, a, true, stream, forced, &Ld, wsb);
+        if (!st) st = matmul_preq_impl(down, m, f, down->L.n, wsb, bytes_b, dst_dev, stream, forced);
+        return st;
+    }
+    st = xnq_matmul_t_silu_gate(gate, up, m, k, f, lhs_dev, workspace_dev, a, h_dev, stream);
+    if (!st) st = matmul_t_ws_impl(down, m, f, down->L.n, h_dev, wsb, bytes_b, dst_dev, stream, forced);
+    return st;
 }
 
 static size_t group_ws_impl(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {

@@ -265,8 +265,13 @@ hipError_t launch_sum_group(const SumGroup& S, uint32_t splits, bool silu, hipSt
 // The skinny kernel over a group of weights of one dtype and K (G.w, G.y,
 // G.count; G.row_end unused) in one launch; `silu` (two weights of one
 // shape) writes silu(x . w0) * (x . w1) to G.y[0] and needs `partial`.
+// `next` (silu only): also quantize the result into the Q8K activation
+// image `next_img` of layout *next (the down projection's input) in the
+// split-sum launch.
 hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
-                               hipStream_t s);
+                               hipStream_t s, const ALayout* next = nullptr, void* next_img = nullptr);
+hipError_t launch_sum_silu_quant(const SumGroup& S, uint32_t splits, size_t m, size_t n, const ALayout& L,
+                                 void* img, hipStream_t s);
 hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                        hipStream_t s);
 

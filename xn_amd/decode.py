@@ -9,7 +9,7 @@ the step on this library:
 
   per layer  q, k, v = x . Wq^T, x . Wk^T, x . Wv^T      one grouped call
              o       = attn . Wo^T
-             h       = silu(o' . Wg^T) * (o' . Wu^T)     one gated call
+             h       = silu(o' . Wg^T) * (o' . Wu^T)     one MLP call
              x_next  = h . Wd^T
   then       logits  = x_L . Wlm^T
 
@@ -163,9 +163,8 @@ class DecodeStep:
             hs = (ctypes.c_void_p * 3)(lw.q.storage.handle, lw.k.storage.handle, lw.v.storage.handle)
             sizes.append(L.xnq_matmul_t_group_workspace_size(hs, 3, self.b))
             sizes.append(L.xnq_qtensor_matmul_t_workspace_size(lw.o.storage.handle, self.b))
-            sizes.append(L.xnq_matmul_t_silu_gate_workspace_size(lw.gate.storage.handle, lw.up.storage.handle,
-                                                                 self.b))
-            sizes.append(L.xnq_qtensor_matmul_t_workspace_size(lw.down.storage.handle, self.b))
+            sizes.append(L.xnq_mlp_t_workspace_size(lw.gate.storage.handle, lw.up.storage.handle,
+                                                    lw.down.storage.handle, self.b))
         sizes.append(L.xnq_qtensor_matmul_t_workspace_size(weights.lm_head.storage.handle, self.b))
         # calls run in stream order, so one workspace serves them all
         self.ws_bytes = max(sizes + [1])
@@ -189,10 +188,8 @@ class DecodeStep:
                                             _ptr(bl["o"]), st))
             if self.glue is not None:
                 self.glue("post_attention", i, bl)
-            check(L.xnq_matmul_t_silu_gate(lw.gate.storage.handle, lw.up.storage.handle, b, d, ff, _ptr(bl["o"]),
-                                           ws, wsn, _ptr(bl["h"]), st))
-            check(L.xnq_qtensor_matmul_t_ws(lw.down.storage.handle, b, ff, d, _ptr(bl["h"]), ws, wsn,
-                                            _ptr(bl["down"]), st))
+            check(L.xnq_mlp_t(lw.gate.storage.handle, lw.up.storage.handle, lw.down.storage.handle, b, d, ff,
+                              _ptr(bl["o"]), ws, wsn, _ptr(bl["h"]), _ptr(bl["down"]), st))
             if self.glue is not None:
                 self.glue("post_mlp", i, bl)
         last = self.bufs[-1]["x_next"] if self.bufs else self.x

@@ -421,6 +421,21 @@ def matmul_t_silu_gate(gate: QTensor, up: QTensor, mkn: Tuple[int, int, int], lh
                                    _ptr(ws) if ws is not None else None, nbytes, _ptr(dst), _stream(gate.device)))
 
 
+def mlp_t(gate: QTensor, up: QTensor, down: QTensor, m: int, lhs: torch.Tensor, h: torch.Tensor,
+          dst: torch.Tensor) -> None:
+    """The SwiGLU MLP of llama.rs:236-264: h = silu(lhs . gate^T) * (lhs . up^T),
+    dst = h . down^T; h [m, f] and dst [m, down rows] are both written.  Runs
+    on the current stream."""
+    k, f = gate.shape()[1], gate.shape()[0]
+    gate._check_mm((m, k, f), lhs, h)
+    down._check_mm((m, f, down.shape()[0]), h, dst)
+    L = _lib.load()
+    nbytes = L.xnq_mlp_t_workspace_size(gate.storage.handle, up.storage.handle, down.storage.handle, m)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gate.device) if nbytes else None
+    check(L.xnq_mlp_t(gate.storage.handle, up.storage.handle, down.storage.handle, m, k, f, _ptr(lhs),
+                      _ptr(ws) if ws is not None else None, nbytes, _ptr(h), _ptr(dst), _stream(gate.device)))
+
+
 def matmul_t_group(qts, m: int, k: int, lhs: torch.Tensor, dsts) -> None:
     """dsts[i][m, n_i] = lhs . qts[i]^T for weights of one dtype and K (the q,
     k, v projections of llama.rs:156-158); one kernel at m = 1."""
