@@ -5,9 +5,9 @@
 // in flight.  This kernel therefore fetches everything a super-block (256
 // columns of K) needs -- the weight chunks and block headers of its columns,
 // the activation tile in MFMA order, d_a and the Q8K block sums -- with
-// global_load_lds DMA into a ring of LDS slots two or three super-blocks
-// ahead of the one being multiplied, so the stream costs no registers and
-// the wavefronts do not wait on a load they issued just before.
+// global_load_lds DMA into a ring of LDS slots, one super-block ahead of the
+// one being multiplied, so the stream costs no registers and the wavefronts
+// do not wait on a load they issued just before.
 //
 // A workgroup of 4 wavefronts owns 128 weight columns (output columns) and a
 // range of super-blocks; wavefront w owns columns 32w .. 32w+31 and all m
@@ -52,8 +52,13 @@ typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 //   da   [64] f32 d_a per row (rows past m repeat the last)
 // The XOR slot order makes the 32 columns' reads of one chunk hit distinct
 // banks while each column's bytes still arrive as one 128-byte line.
+// Two slots: the smaller LDS footprint lets two or three workgroups share a
+// CU, and their barriers and expansion interleave, which beats a deeper
+// ring in one workgroup (batch-16 decode step 2633 us with four slots, 2581
+// with three, 2514 with two).  A larger XNQ_SKINNY_RING_MAX at build time
+// deepens it where the LDS allows.
 #ifndef XNQ_SKINNY_RING_MAX
-#define XNQ_SKINNY_RING_MAX 4
+#define XNQ_SKINNY_RING_MAX 2
 #endif
 constexpr int kRingMax = XNQ_SKINNY_RING_MAX;
 
@@ -608,12 +613,17 @@ static int skinny_waves(size_t m, size_t n, size_t k) {
 }
 
 uint32_t skinny_splits(size_t m, size_t n, size_t k) {
-    // the LDS ring takes most of a CU, so one workgroup per CU: split K while
-    // the grid still fits the 256 CUs at once, each split at least two
-    // super-blocks long
+    // split K while the grid still has about one workgroup per CU, each split
+    // at least two super-blocks long (more splits, for two or three
+    // workgroups per CU, measured slower: batch-16 decode step 2514 us at
+    // 256, 2715 at 512; XNQ_SKINNY_WG_TARGET overrides the 256, tuning)
     const size_t tiles = (n + 32 * skinny_waves(m, n, k) - 1) / (32 * skinny_waves(m, n, k));
     const size_t nsb = k / 256;
-    size_t splits = 256 / tiles;
+    static const size_t target = [] {
+        const char* e = getenv("XNQ_SKINNY_WG_TARGET");
+        return e && atoi(e) > 0 ? (size_t)atoi(e) : (size_t)256;
+    }();
+    size_t splits = target / tiles;
     if (splits > nsb / 2) splits = nsb / 2;
     return splits < 1 ? 1u : (uint32_t)splits;
 }
