@@ -432,32 +432,37 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
 }
 
 // Automatic routes (measured on MI355X):
-//   m <= 8 (Q4K: m < 6 when
-//   n >= 8192, m < 8 when k >= 8192) matvec kernels (up to 8 rows per launch)
-//   m <= 64                          skinny int8-MFMA kernel for Q4K / Q6K
-//   larger m                         tiled int8-MFMA prefill kernel
+//   m <= 8 matvec kernels (up to 8 rows per launch), except where the skinny
+//     kernel is faster: from m = 5 on Q4K / Q6K weights with n >= 8192 or
+//     k >= 8192, from m = 3 for a group of weights sharing one activation
+//     (q/k/v, gate/up) that joins at least 6144 columns
+//   m <= 64  skinny int8-MFMA kernel for Q4K / Q6K
+//   larger m tiled int8-MFMA prefill kernel
 // Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MIN_ROWS and
 // XNQ_SKINNY_MAX_ROWS override the skinny range for tuning (read once per
-// process); `forced` is xnq_set_route's override as read at the entry point.
+// process); `forced` is xnq_set_route's override as read at the entry point;
+// `group_n` is the joined width of a group (0 for a single weight).
 enum Route { kMatvec, kSkinny, kMfma };
 
-static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced) {
+static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced, size_t group_n = 0) {
     static const size_t skinny_min = env_size("XNQ_SKINNY_MIN_ROWS", 0);
     const size_t skinny_max = skinny_max_rows();
     if (forced == 1) return kMatvec;
     if (forced == 2) return kMfma;
     if (forced == 3) return kSkinny;
-    // measured crossovers: the matvec kernels' cost grows with every row and
-    // past 8 rows takes a second launch, the skinny kernel's hardly grows
-    // below 32 rows (4096 x 4096: matvec 8.5 us at m = 8, 12.8 at m = 10,
-    // skinny 10.0 at both; 14336 -> 4096 Q6_K: 23.5 against 26.6 at m = 8;
-    // 4096 -> 14336 Q4_K: 21.3 against 17.7 at m = 6; 14336 -> 4096 Q4_K,
-    // whose skinny expansion is cheaper than Q6_K's: 20.1 against 18.9 at m = 8)
-    const size_t skinny_lo = skinny_min               ? skinny_min
-                             : dtype != XNQ_Q4K        ? 9
-                             : n >= 8192               ? 6
-                             : k >= 8192               ? 8
-                                                       : 9;
+    // measured crossovers (graph steps, µs, matvec against skinny): the
+    // matvec kernels' cost jumps from 4 to 5 rows (the 8-row template) and
+    // past 8 rows takes a second launch; the skinny kernel's hardly grows
+    // below 32 rows.  4096 -> 14336 Q4_K at m = 5: 18.9 against 17.5;
+    // 14336 -> 4096 Q4_K 25.5 against 18.8, Q6_K 26.3 against 24.3;
+    // 4096 -> 128256 Q6_K 186 against 119; 4096 x 4096 at m = 8 10.7
+    // against 13.2 (matvec up to 8 rows).  Groups: gate/up pair at m = 3
+    // 28.5 against 24.6, q/k/v 18.0 against 14.0; at m = 2 the matvec wins
+    // (22.1 against 25.5, 13.5 against 14.2).
+    const size_t skinny_lo = skinny_min                      ? skinny_min
+                             : group_n >= 6144               ? 3
+                             : n >= 8192 || k >= 8192        ? 5
+                                                             : 9;
     if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
     if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
     return kMatvec;
@@ -701,22 +706,25 @@ static bool shared_quantize(const xnq_qtensor* const* qts, size_t count, size_t 
     return true;
 }
 
+static size_t joined_n(const xnq_qtensor* const* qts, size_t count) {
+    size_t n = 0;
+    for (size_t i = 0; i < count; i++) n += qts[i]->L.n;
+    return n;
+}
+
 // Weights that share one quantize and all take the skinny route run as one
 // skinny launch over their joined column tiles, with one split-K sum.
 static bool skinny_group(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
     if (!shared_quantize(qts, count, m, forced)) return false;
     for (size_t i = 0; i < count; i++) {
         const WLayout& L = qts[i]->L;
-        if (pick_route(L.dtype, m, L.n, L.k, forced) != kSkinny || !skinny_supported(L.dtype, m, L.n, L.k)) return false;
+        if (pick_route(L.dtype, m, L.n, L.k, forced, joined_n(qts, count)) != kSkinny ||
+            !skinny_supported(L.dtype, m, L.n, L.k))
+            return false;
     }
     return true;
 }
 
-static size_t joined_n(const xnq_qtensor* const* qts, size_t count) {
-    size_t n = 0;
-    for (size_t i = 0; i < count; i++) n += qts[i]->L.n;
-    return n;
-}
 
 // Activation image, then one partial region per weight ([split][m][n_t]).
 static size_t skinny_group_ws(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
