@@ -163,7 +163,9 @@ def test_matmul_small(orc, dev, dt, m, entry):
     (Q4K, 4096, 1792),    # an 8-way column-parallel shard of gate/up
     (Q6K, 1792, 4096),    # an 8-way row-parallel shard of down
 ])
-@pytest.mark.parametrize("m", [1, 4, 8])  # m = 8: matvec for Q6_K and 4096 x 4096, skinny for Q4_K K = 14336
+# m = 5 and 8: the skinny kernel for Q4_K / Q6_K with N or K >= 8192, the
+# matvec for 4096 x 4096, the shards and the other dtypes
+@pytest.mark.parametrize("m", [1, 4, 5, 8])
 def test_matmul_config_shapes(orc, dev, dt, k, n, m):
     rng = np.random.default_rng(7000 + dt + k + n + m)
     w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
@@ -321,6 +323,35 @@ def test_matmul_group(orc, dev, dt, m, ns):
     matmul_t_group(qts, m, k, torch.from_numpy(x).to(dev), dsts)
     for i, (b, n) in enumerate(zip(blocks, ns)):
         assert_close(dsts[i].cpu().numpy(), orc.matmul(dt, x, b, n), f"group dt={dt} m={m} weight {i} n={n}")
+
+
+@pytest.mark.parametrize("m", [2, 3, 5])
+def test_group_decode_shapes(orc, dev, m):
+    """q/k/v (4096 -> 4096, 1024, 1024) and the gate/up pair (4096 -> 14336)
+    of config 5 at few rows: one joined skinny launch from m = 3, the
+    matvec at m = 2."""
+    from xn_amd.quantized import matmul_t_group, matmul_t_silu_gate
+
+    k = 4096
+    rng = np.random.default_rng(8300 + m)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    ns = (4096, 1024, 1024)
+    blocks = [orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)).astype(np.float32)) for n in ns]
+    qts = [upload(b, n, k, Q4K, dev) for b, n in zip(blocks, ns)]
+    dsts = [torch.full((m, n), float("nan"), dtype=torch.float32, device=dev) for n in ns]
+    matmul_t_group(qts, m, k, xd, dsts)
+    for i, (b, n) in enumerate(zip(blocks, ns)):
+        assert_close(dsts[i].cpu().numpy(), orc.matmul(Q4K, x, b, n), f"qkv m={m} weight {i}")
+    del qts, blocks
+    n = 14336
+    gb = orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    ub = orc.from_float(Q4K, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    g, u = upload(gb, n, k, Q4K, dev), upload(ub, n, k, Q4K, dev)
+    dst = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    matmul_t_silu_gate(g, u, (m, k, n), xd, dst)
+    want = _silu(orc.matmul(Q4K, x, gb, n).astype(np.float64)) * orc.matmul(Q4K, x, ub, n)
+    assert_close(dst.cpu().numpy(), want, f"gate/up m={m}")
 
 
 def test_matmul_group_mixed_dtypes(orc, dev):
