@@ -9,15 +9,16 @@
 // one being multiplied, so the stream costs no registers and the wavefronts
 // do not wait on a load they issued just before.
 //
-// A workgroup of 4 wavefronts owns 128 weight columns (output columns) and a
-// range of super-blocks; wavefront w owns columns 32w .. 32w+31 and all m
-// activation rows (one or two 32-row MFMA tiles).  Per super-block each
-// wavefront expands its columns' chunks from LDS into the two int8 digit
-// planes of the prefill kernel (Q4K: sc = 8*sh + sl, digits sh*q and sl*q;
-// Q6K: sc*(q-32) = 128*hi + lo), contracts them with the activation tile on
-// v_mfma_i32_32x32x32_i8 and applies d_a * d_w in an f32 epilogue; the Q4K
-// min term is a K = 8 GEMM of -d_a*bsum32 by dmin*m_j on the bf16 matrix
-// cores.  The integer sums per super-block are exact, as in the reference's
+// A workgroup of NW = 4 or 8 wavefronts owns 32 * NW weight columns (output
+// columns) and a range of super-blocks; wavefront w owns columns 32w ..
+// 32w+31 and all m activation rows: up to 16 rows one 16-row tile on
+// v_mfma_i32_16x16x64_i8 (two 16-column tiles per wavefront, compute16),
+// above that one or two 32-row tiles on v_mfma_i32_32x32x32_i8.  Per
+// super-block each wavefront expands its columns' chunks from LDS into the
+// two int8 digit planes of the prefill kernel (Q4K: sc = 8*sh + sl, digits
+// sh*q and sl*q; Q6K: sc*(q-32) = 128*hi + lo), contracts them with the
+// activation tile and applies d_a * d_w in an f32 epilogue; the Q4K min term
+// is a GEMM of -d_a*bsum32 by dmin*m_j on the bf16 matrix cores.  The integer sums per super-block are exact, as in the reference's
 // block dots (k_quants.rs:1337-1416, 1743-1798).  When the column tiles alone
 // do not fill the GPU, the super-blocks are split across workgroups and the
 // partial outputs are summed in split order afterwards.
@@ -41,12 +42,15 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
-// LDS slot of one super-block (byte offsets).  R = 32 * MT activation rows.
-//   wq   [col 128][slot 8][16]  weight chunk (slot ^ (col & 7)) of the column
-//   hdr  [wave 4][lane 64][16]  Q4K: d | dmin, scales[12]; Q6K: int8 scales[16]
-//                               of the wavefront's column lane & 31
-//   wh   Q6K [col 128][slot 4][16]  high-bit words of chunks 2p, 2p+1, p = slot ^ (col & 3)
-//   wd   Q6K [wave 4][lane 64] dword holding the f16 d of super-blocks 2j, 2j+1
+// LDS slot of one super-block (byte offsets).  R = 16 activation rows for
+// MT == 0 (16-row tiles), else 32 * MT; C = 32 * NW columns.
+//   wq   [col C][slot 8][16]  weight chunk (slot ^ (col & 7)) of the column
+//   hdr  Q4K: d | dmin, scales[12]; Q6K: int8 scales[16]; 16-row tiles
+//        [col C][16], else [wave NW][lane 64][16] (the wavefront's column
+//        lane & 31)
+//   wh   Q6K [col C][slot 4][16]  high-bit words of chunks 2p, 2p+1, p = slot ^ (col & 3)
+//   wd   Q6K dword holding the f16 d of super-blocks 2j, 2j+1: 16-row tiles
+//        [col C], else [wave NW][lane 64]
 //   act  [chunk 8][half 2][row R][16]  activation quants in MFMA A order
 //   bs   Q4K [row R][part 2][16]   chunk bsum pairs of sub-blocks 4*part .. +3
 //   da   [64] f32 d_a per row (rows past m repeat the last)
