@@ -193,9 +193,8 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
 // 64-element step, that is half g & 1 of chunk 2*ks + (g >> 1); the
 // accumulator holds rows 4g .. 4g+3 of column l & 15.  Digit planes,
 // epilogue and min term as in the 32-row path (skinny_kernel).
-template <int DT, int NW>
+template <int DT, class L>
 __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint32_t lane, bool odd_sb, v4f* acc) {
-    using L = KLay<DT, 0, NW>;
     constexpr bool kQ4K = L::kQ4K;
     constexpr int kShift = kQ4K ? 3 : 7;
     const uint32_t g = lane >> 4, li = lane & 15, h = g & 1;
@@ -431,7 +430,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 
         const uint8_t* S = lds + (i % kRing) * L::kSlot;
         if constexpr (MT == 0) {
-            compute16<DT, NW>(S, wave, lane, ((sb0 + i) & 1) != 0, acc16);
+            compute16<DT, L>(S, wave, lane, ((sb0 + i) & 1) != 0, acc16);
         } else {
         const uint32_t cl = wave * 32 + lrow;
         const uint4 hdr = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 64 + lrow) * 16);
@@ -560,6 +559,197 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     }
 }
 
+// ---------------------------------------------------------------------------
+// 16-row tiles with K split over the wavefronts of one workgroup instead of
+// over workgroups: every wavefront of a workgroup owns the same 32 columns
+// and super-blocks wave, wave + NW, ...; it streams them through D LDS slots
+// of its own (weights, block headers, the activation tile, d_a and bsums, all
+// by DMA), so it never waits for another wavefront until the end, where the
+// NW partial sums are added in wavefront order in LDS and stored.  No split-K
+// partials and no sum launch.
+
+// One wavefront's LDS slot (byte offsets; the compute16 layout for one
+// wavefront of 32 columns, wave index 0).
+template <int DT>
+struct WkLay {
+    static constexpr bool kQ4K = DT == XNQ_Q4K;
+    static constexpr int kCols = 32;
+    static constexpr int kWq = 0;                            // [col 32][slot 8][16]
+    static constexpr int kHdr = kWq + kCols * 128;           // [col 32][16]
+    static constexpr int kWh = kHdr + kCols * 16;            // Q6K [col 32][slot 4][16]
+    static constexpr int kWd = kWh + (kQ4K ? 0 : kCols * 64);  // Q6K [col 32] dword (+128 B for lanes 32..63)
+    static constexpr int kAct = kWd + (kQ4K ? 0 : 64 * 4);   // [chunk 8][half 2][row 16][16]
+    static constexpr int kBs = kAct + 8 * 2 * 16 * 16;       // Q4K [row 16][part 2][16]
+    static constexpr int kDa = kBs + (kQ4K ? 16 * 32 : 0);   // [64] f32
+    static constexpr int kSlot = kDa + 64 * 4;
+    // DMA instructions per super-block: weights, header (two dword DMAs),
+    // (Q6K: high bits, d), activation, (Q4K: bsums, two dword DMAs), d_a
+    static constexpr int kD = kQ4K ? 4 + 2 + 4 + 2 + 1 : 4 + 2 + 2 + 1 + 4 + 1;
+};
+
+template <int DT, int NW, int D>
+__global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, AView a, uint32_t m) {
+    using L = WkLay<DT>;
+    constexpr bool kQ4K = L::kQ4K;
+    static_assert((D - 2) * L::kD < 64, "vmcnt range");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t bx = blockIdx.x;
+    const uint32_t t = G.count > 1 && bx >= O.tile_end[0] ? (G.count > 2 && bx >= O.tile_end[1] ? 2u : 1u) : 0u;
+    const WView w = G.w[t];
+    float* __restrict__ y = O.y[t];
+    const uint32_t col0 = (bx - (t > 0 ? O.tile_end[t - 1] : 0u)) * L::kCols;
+    const uint32_t nsb_all = w.k / 256;
+    const uint32_t nsb = wave < nsb_all ? (nsb_all - wave + NW - 1) / NW : 0u;  // this wavefront's super-blocks
+    const uint32_t lbase = (uint32_t)(uintptr_t)lds + wave * D * L::kSlot;
+    const ActImg& A = a.A;
+    const uint32_t cmax = w.n - 1, rmax = m - 1;
+
+    // per-lane DMA offsets (lanes past the last column or row re-read the last one)
+    uint32_t oq[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t cl = 8 * j + (lane >> 3);
+        oq[j] = min(col0 + cl, cmax) * w.q_row + ((lane & 7) ^ (cl & 7)) * 16;
+    }
+    // headers: dword lane & 3 of column 16 j + lane / 4 (two dword DMAs, j = 0, 1);
+    // Q6K d: column lane & 31 (lanes 32..63 repeat columns 0..31 into the
+    // second half of the 256-byte region)
+    const uint32_t os0 = kq_tile_off(w.nb, min(col0 + (lane >> 2), cmax), 0, 16) + (lane & 3) * 4;
+    const uint32_t os1 = kq_tile_off(w.nb, min(col0 + 16 + (lane >> 2), cmax), 0, 16) + (lane & 3) * 4;
+    const uint32_t od = kq_tile_off((w.nb + 1) / 2, min(col0 + (lane & 31), cmax), 0, 4);
+    uint32_t oh[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t cl = 16 * j + (lane >> 2);
+        oh[j] = kQ4K ? 0u : min(col0 + cl, cmax) * w.h_row + ((lane & 3) ^ (cl & 3)) * 16;
+    }
+    uint32_t oa[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t p = j * 4 + (lane >> 4);  // piece = (chunk p / 2, half p & 1), lane & 15 = row
+        oa[j] = min(lane & 15, rmax) * A.row_bytes + (p & 1) * (A.k / 2) + (p >> 1) * 16;
+    }
+    // bsums of rows 0..15: dword lane & 7 of row 8 j + lane / 8 (two dword DMAs)
+    const uint32_t obs0 = min(lane >> 3, rmax) * A.row_bytes + A.s_off + (lane & 7) * 4;
+    const uint32_t obs1 = min(8 + (lane >> 3), rmax) * A.row_bytes + A.s_off + (lane & 7) * 4;
+    const uint32_t oda = min(lane, rmax) * A.row_bytes + A.d_off;
+
+    auto issue = [&](uint32_t i) {
+        const uint32_t sb = wave + i * NW;
+        const uint32_t slot = lbase + (i % D) * L::kSlot;
+#pragma unroll
+        for (int j = 0; j < 4; j++) dma16(w.q + sb * 128, oq[j], slot + L::kWq + 8 * j * 128);
+        dma4(w.st + sb * 16 * 128, os0, slot + L::kHdr);
+        dma4(w.st + sb * 16 * 128, os1, slot + L::kHdr + 256);
+        if (!kQ4K) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + 16 * j * 64);
+            dma4(w.dt + (sb >> 1) * 512, od, slot + L::kWd);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) dma16(a.img + sb * 128, oa[j], slot + L::kAct + j * 1024);
+        if (kQ4K) {
+            dma4(a.img + sb * 32, obs0, slot + L::kBs);
+            dma4(a.img + sb * 32, obs1, slot + L::kBs + 256);
+        }
+        dma4(a.img + sb * 4, oda, slot + L::kDa);
+    };
+
+    v4f acc[2] = {v4f{}, v4f{}};
+#pragma unroll
+    for (int i = 0; i < D - 1; i++)
+        if ((uint32_t)i < nsb) issue(i);
+    for (uint32_t i = 0; i < nsb; i++) {
+        wait_younger<L::kD, D - 2>(min((uint32_t)(D - 2), nsb - 1 - i));
+        // slot (i - 1) % D was read by this wavefront's last compute, whose
+        // LDS reads have all been consumed; the asm barrier of the DMA keeps
+        // them ahead of it
+        if (i + D - 1 < nsb) issue(i + D - 1);
+        compute16<DT, L>(lds + (lbase - (uint32_t)(uintptr_t)lds) + (i % D) * L::kSlot, 0, lane,
+                         ((wave + i * NW) & 1) != 0, acc);
+    }
+
+    // the wavefronts' sums, added in wavefront order
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);
+    if (wave > 0) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+            *reinterpret_cast<v4f*>(red + (((wave - 1) * 2 + ct) * 64 + lane) * 4) = acc[ct];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (uint32_t v = 1; v < (uint32_t)NW; v++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) acc[ct] += *reinterpret_cast<const v4f*>(red + (((v - 1) * 2 + ct) * 64 + lane) * 4);
+    const uint32_t g = lane >> 4;
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++) {
+        const uint32_t col = col0 + ct * 16 + (lane & 15);
+        if (col < w.n) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t row = 4 * g + e;
+                if (row < m) y[(size_t)row * w.n + col] = acc[ct][e];
+            }
+        }
+    }
+}
+
+
+template <int DT, int NW, int D>
+hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* partial, bool silu, hipStream_t s,
+                            const ALayout* next, void* next_img) {
+    using L = WkLay<DT>;
+    constexpr uint32_t kLds = (uint32_t)(NW * D * L::kSlot);
+    static_assert(kLds <= 160 * 1024, "LDS budget");
+    static_assert(NW * D * L::kSlot >= (NW - 1) * 2 * 64 * 16, "reduction area");
+    {
+        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(skinny_wk_kernel<DT, NW, D>), kLds);
+        if (e != hipSuccess) return e;
+    }
+    SkOut O{};
+    SumGroup S{};
+    uint32_t tiles = 0;
+    size_t off = 0;
+    for (uint32_t t = 0; t < G.count; t++) {
+        const size_t cnt = m * (size_t)G.w[t].n;
+        tiles += (G.w[t].n + L::kCols - 1) / L::kCols;
+        O.tile_end[t] = tiles;
+        O.y[t] = silu ? partial + off : G.y[t];
+        S.part[t] = partial + off;
+        S.y[t] = G.y[t];
+        S.cnt[t] = cnt;
+        off += cnt;
+    }
+    S.count = G.count;
+    hipLaunchKernelGGL((skinny_wk_kernel<DT, NW, D>), dim3(tiles), dim3(64 * NW), kLds, s, G, O, a, (uint32_t)m);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !silu) return e;
+    if (next) return launch_sum_silu_quant(S, 1, m, G.w[0].n, *next, next_img, s);
+    return launch_sum_group(S, 1, true, s);
+}
+
+// The wavefront-split kernel where it measured faster than the split-K one
+// plus its sum launch (graph steps at m = 16, µs): Q4_K with K <= 4096 and at
+// most 512 column tiles, which two workgroups per CU cover in one round
+// (4096 x 4096 13.4 -> 11.4, the q/k/v group 15.0 -> 12.1, 4096 -> 14336
+// 18.3 -> 16.7; batch-16 decode step 2520 -> 2378).  Longer K leaves each
+// wavefront a long serial chain (14336 -> 4096 Q4_K 19.4 -> 22.3), more
+// tiles take two rounds (the gate/up pair 25.5 -> 29.9), and the Q6_K slot
+// is too large for two workgroups per CU (14336 -> 4096 24.7 -> 32.3).
+// XNQ_SKINNY_WK=0 turns it off (tuning).
+static bool skinny_wk(uint32_t dtype, size_t tiles32, size_t k) {
+    static const bool on = [] {
+        const char* e = getenv("XNQ_SKINNY_WK");
+        return !e || atoi(e) != 0;
+    }();
+    return on && dtype == XNQ_Q4K && k <= 4096 && tiles32 <= 512;
+}
+
 template <int DT, int MT, int NW>
 hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t splits, float* partial, bool silu,
                             hipStream_t s, const ALayout* next, void* next_img) {
@@ -653,11 +843,16 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
     if (m > 64 || G.count > (uint32_t)kMaxGroup || (silu && G.count != 2)) return hipErrorInvalidValue;
     if (silu && !partial) return hipErrorInvalidValue;
     if (splits > 1 && !partial) splits = 1;
-    size_t n = 0;
-    for (uint32_t t = 0; t < G.count; t++) n += G.w[t].n;
+    size_t n = 0, tiles32 = 0;
+    for (uint32_t t = 0; t < G.count; t++) {
+        n += G.w[t].n;
+        tiles32 += (G.w[t].n + 31) / 32;
+    }
     const bool w8 = skinny_waves(m, n, G.w[0].k) == 8;
 #define XNQ_SK(DT)                                                                                   \
     if (G.w[0].dtype == DT) {                                                                        \
+        if (m <= 16 && skinny16() && skinny_wk(DT, tiles32, G.w[0].k) && (!silu || partial))       \
+            return launch_skinny_wk<DT, 4, 2>(G, a, m, partial, silu, s, next, next_img);             \
         if (m <= 16 && skinny16())                                                                 \
             return w8 ? launch_skinny_dt<DT, 0, 8>(G, a, m, splits, partial, silu, s, next, next_img)               \
                       : launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s, next, next_img);              \
