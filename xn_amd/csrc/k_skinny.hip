@@ -734,20 +734,23 @@ hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* pa
 }
 
 // The wavefront-split kernel where it measured faster than the split-K one
-// plus its sum launch (graph steps at m = 16, µs): Q4_K with K <= 4096 and at
-// most 512 column tiles, which two workgroups per CU cover in one round
-// (4096 x 4096 13.4 -> 11.4, the q/k/v group 15.0 -> 12.1, 4096 -> 14336
-// 18.3 -> 16.7; batch-16 decode step 2520 -> 2378).  Longer K leaves each
-// wavefront a long serial chain (14336 -> 4096 Q4_K 19.4 -> 22.3), more
-// tiles take two rounds (the gate/up pair 25.5 -> 29.9), and the Q6_K slot
-// is too large for two workgroups per CU (14336 -> 4096 24.7 -> 32.3).
-// XNQ_SKINNY_WK=0 turns it off (tuning).
+// plus its sum launch (graph steps at m = 16, µs): K <= 4096 and at most 512
+// column tiles of 32, which two workgroups per CU (Q4_K) or one round and a
+// half (Q6_K) cover: Q4_K 4096 x 4096 13.4 -> 11.4, the q/k/v group 15.0 ->
+// 12.1, 4096 -> 14336 18.3 -> 16.7; Q6_K 1792 -> 4096 14.8 -> 10.5, 2048 ->
+// 8192 15.1 -> 11.8, 4096 -> 14336 26.1 -> 25.7; batch-16 decode step 2520
+// -> 2376.  Longer K leaves each wavefront a long serial chain (14336 ->
+// 4096 Q4_K 19.4 -> 22.3, Q6_K 24.7 -> 32.3) and more tiles take extra
+// rounds (the gate/up pair 25.5 -> 29.9, the Q6_K lm_head 125 -> 164).
+// XNQ_SKINNY_WK=0 turns it off, 2 forces it for every 16-row launch (tuning).
 static bool skinny_wk(uint32_t dtype, size_t tiles32, size_t k) {
-    static const bool on = [] {
+    static const int mode = [] {
         const char* e = getenv("XNQ_SKINNY_WK");
-        return !e || atoi(e) != 0;
+        return e ? atoi(e) : 1;
     }();
-    return on && dtype == XNQ_Q4K && k <= 4096 && tiles32 <= 512;
+    if (mode == 2) return true;
+    (void)dtype;
+    return mode != 0 && k <= 4096 && tiles32 <= 512;
 }
 
 template <int DT, int MT, int NW>
