@@ -199,9 +199,12 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
     constexpr int kShift = kQ4K ? 3 : 7;
     const uint32_t g = lane >> 4, li = lane & 15, h = g & 1;
     uint4 hdr[2];
+    Q4KScales qs[2];
 #pragma unroll
-    for (int ct = 0; ct < 2; ct++)
+    for (int ct = 0; ct < 2; ct++) {
         hdr[ct] = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 32 + ct * 16 + li) * 16);
+        if (kQ4K) qs[ct] = q4k_scales(hdr[ct].y, hdr[ct].z, hdr[ct].w);
+    }
     v4i hi[2], lo[2];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
@@ -214,9 +217,9 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
             const uint32_t q4[4] = {qc.x, qc.y, qc.z, qc.w};
             uint32_t p0[4], p1[4];
             if (kQ4K) {
-                int sc, mn;
-                q4k_scale_min(hdr[ct].y, hdr[ct].z, hdr[ct].w, c, sc, mn);
-                const uint32_t sh = (uint32_t)sc >> 3, sl = (uint32_t)sc & 7;
+                // scale of sub-block c = 2 ks + (g >> 1): dword by ks, byte by lane
+                const uint32_t sc = ((ks < 2 ? qs[ct].sc_lo : qs[ct].sc_hi) >> (8 * ((2 * ks) & 3) + 8 * (g >> 1))) & 0xffu;
+                const uint32_t sh = sc >> 3, sl = sc & 7;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const uint32_t nib = (q4[j] >> (4 * h)) & 0x0F0F0F0Fu;
@@ -283,10 +286,9 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
             // (mh0, mh0, mh1, mh1, ml0, ml0, ml1, ml1): the 8-term dot with a8
             // is (ah0 + al0)(mh0 + ml0) + (ah1 + al1)(mh1 + ml1)
             const float dm = f16_bits_to_f32(hdr[ct].x >> 16);
-            int sc0, mn0, sc1, mn1;
-            q4k_scale_min(hdr[ct].y, hdr[ct].z, hdr[ct].w, (int)(2 * g), sc0, mn0);
-            q4k_scale_min(hdr[ct].y, hdr[ct].z, hdr[ct].w, (int)(2 * g + 1), sc1, mn1);
-            const float w0 = dm * (float)mn0, w1 = dm * (float)mn1;
+            // mins of sub-blocks 2g, 2g + 1: bytes 2 (g & 1), +1 of m_lo (g < 2) or m_hi
+            const uint32_t mw = (g < 2 ? qs[ct].m_lo : qs[ct].m_hi) >> (16 * (g & 1));
+            const float w0 = dm * (float)(mw & 0xffu), w1 = dm * (float)((mw >> 8) & 0xffu);
             const __bf16 h0 = (__bf16)w0, h1 = (__bf16)w1;
             const __bf16 l0 = (__bf16)(w0 - (float)h0), l1 = (__bf16)(w1 - (float)h1);
             const v8bf b8 = {h0, h0, h1, h1, l0, l0, l1, l1};

@@ -106,6 +106,23 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+// All eight 6-bit scales and mins of a Q4K block header at once, four per
+// dword: byte r of sc_lo / sc_hi is the scale of sub-block r / 4 + r, the
+// same for m_lo / m_hi (the get_scale_min_k4 cases of utils.rs:53-63 applied
+// bytewise: j < 4 takes the low 6 bits of q[j] and q[j + 4]; j >= 4 takes a
+// nibble of q[j + 4] and the top 2 bits of q[j - 4] resp. q[j]).
+struct Q4KScales {
+    uint32_t sc_lo, sc_hi, m_lo, m_hi;
+};
+__host__ __device__ __forceinline__ Q4KScales q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2) {
+    Q4KScales q;
+    q.sc_lo = s0 & 0x3f3f3f3fu;
+    q.sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    q.m_lo = s1 & 0x3f3f3f3fu;
+    q.m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    return q;
+}
+
 // The 16 six-bit Q3K scales (0..63): byte g of the aux words that
 // k_quants.rs:1252-1258 builds from the 12 packed bytes s0, s1, s2.
 __device__ __forceinline__ int q3k_scale(uint32_t s0, uint32_t s1, uint32_t s2, int g) {
