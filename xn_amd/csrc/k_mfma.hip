@@ -258,9 +258,10 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ void q6_digits(uint32_t q, int sc, uint32_t& lo, uint32_t& hi) {
     const v2s x01 = {(short)(q & 0xFF), (short)((q >> 8) & 0xFF)};
     const v2s x23 = {(short)((q >> 16) & 0xFF), (short)(q >> 24)};
-    const v2s off = {32, 32};
+    // (q - 32) * sc as q * sc + (-32 sc): one packed multiply-add per pair
     const v2s s2 = {(short)sc, (short)sc};
-    const v2s w01 = (x01 - off) * s2, w23 = (x23 - off) * s2;
+    const v2s c2 = {(short)(-32 * sc), (short)(-32 * sc)};
+    const v2s w01 = x01 * s2 + c2, w23 = x23 * s2 + c2;
     const v2s m7 = {127, 127};
     const v2s l01 = w01 & m7, l23 = w23 & m7;
     const v2s h01 = w01 >> 7, h23 = w23 >> 7;
