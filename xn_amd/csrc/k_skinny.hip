@@ -495,13 +495,12 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
         v8bf bh8, bl8;
         if (kQ4K) {
             const float dm = f16_bits_to_f32(hdr.x >> 16);
+            // mins of sub-blocks 4 half .. 4 half + 3: the bytes of m_lo / m_hi
+            const Q4KScales qs = q4k_scales(hdr.y, hdr.z, hdr.w);
+            const uint32_t mw = half ? qs.m_hi : qs.m_lo;
             float v[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                int sc2, mn2;
-                q4k_scale_min(hdr.y, hdr.z, hdr.w, (int)(4 * half + u), sc2, mn2);
-                v[u] = dm * (float)mn2;
-            }
+            for (int u = 0; u < 4; u++) v[u] = dm * (float)((mw >> (8 * u)) & 0xffu);
             const uint4 bv = bf16_split4(v);
             bh8 = __builtin_bit_cast(v8bf, make_uint4(bv.x, bv.y, bv.x, bv.y));
             bl8 = __builtin_bit_cast(v8bf, make_uint4(bv.z, bv.w, bv.z, bv.w));
