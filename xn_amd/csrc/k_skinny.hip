@@ -188,31 +188,31 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
     return make_uint4(hu.x, hu.y, lu.x, lu.y);
 }
 
-// One super-block of a 16-row tile (m <= 16) for wavefront `wave`'s 32
-// columns, as two 16-column tiles on v_mfma_i32_16x16x64_i8: lane l holds
+// One super-block of a 16-row tile (m <= 16) for wavefront `wave`'s 16 * TC
+// columns, as TC 16-column tiles on v_mfma_i32_16x16x64_i8: lane l holds
 // row / column l & 15 and the 16-element K slice g = l >> 4 of each
 // 64-element step, that is half g & 1 of chunk 2*ks + (g >> 1); the
 // accumulator holds rows 4g .. 4g+3 of column l & 15.  Digit planes,
 // epilogue and min term as in the 32-row path (skinny_kernel).
-template <int DT, class L>
+template <int DT, class L, int TC = 2>
 __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint32_t lane, bool odd_sb, v4f* acc) {
     constexpr bool kQ4K = L::kQ4K;
     constexpr int kShift = kQ4K ? 3 : 7;
     const uint32_t g = lane >> 4, li = lane & 15, h = g & 1;
-    uint4 hdr[2];
-    Q4KScales qs[2];
+    uint4 hdr[TC];
+    Q4KScales qs[TC];
 #pragma unroll
-    for (int ct = 0; ct < 2; ct++) {
+    for (int ct = 0; ct < TC; ct++) {
         hdr[ct] = *reinterpret_cast<const uint4*>(S + L::kHdr + (wave * 32 + ct * 16 + li) * 16);
         if (kQ4K) qs[ct] = q4k_scales(hdr[ct].y, hdr[ct].z, hdr[ct].w);
     }
-    v4i hi[2], lo[2];
+    v4i hi[TC], lo[TC];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const int c = 2 * ks + (int)(g >> 1);
         const v4i av = *reinterpret_cast<const v4i*>(S + L::kAct + ((4 * ks + g) * 16 + li) * 16);
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++) {
+        for (int ct = 0; ct < TC; ct++) {
             const uint32_t cl = wave * 32 + ct * 16 + li;
             const uint4 qc = *reinterpret_cast<const uint4*>(S + L::kWq + cl * 128 + ((c ^ (cl & 7)) * 16));
             const uint32_t q4[4] = {qc.x, qc.y, qc.z, qc.w};
@@ -269,7 +269,7 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
         a8 = v8bf{h0, l0, h1, l1, h0, l0, h1, l1};
     }
 #pragma unroll
-    for (int ct = 0; ct < 2; ct++) {
+    for (int ct = 0; ct < TC; ct++) {
         float dw;
         if (kQ4K) {
             dw = f16_bits_to_f32(hdr[ct].x & 0xffffu);
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 
 // ---------------------------------------------------------------------------
 // 16-row tiles with K split over the wavefronts of one workgroup instead of
-// over workgroups: every wavefront of a workgroup owns the same 32 columns
+// over workgroups: every wavefront of a workgroup owns the same 16 * TC columns
 // and super-blocks wave, wave + NW, ...; it streams them through D LDS slots
 // of its own (weights, block headers, the activation tile, d_a and bsums, all
 // by DMA), so it never waits for another wavefront until the end, where the
@@ -571,27 +571,28 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 // partials and no sum launch.
 
 // One wavefront's LDS slot (byte offsets; the compute16 layout for one
-// wavefront of 32 columns, wave index 0).
-template <int DT>
+// wavefront of C = 16 * TC columns, wave index 0).
+template <int DT, int TC>
 struct WkLay {
     static constexpr bool kQ4K = DT == XNQ_Q4K;
-    static constexpr int kCols = 32;
-    static constexpr int kWq = 0;                            // [col 32][slot 8][16]
-    static constexpr int kHdr = kWq + kCols * 128;           // [col 32][16]
-    static constexpr int kWh = kHdr + kCols * 16;            // Q6K [col 32][slot 4][16]
-    static constexpr int kWd = kWh + (kQ4K ? 0 : kCols * 64);  // Q6K [col 32] dword (+128 B for lanes 32..63)
+    static constexpr int kCols = 16 * TC;
+    static constexpr int kWq = 0;                            // [col C][slot 8][16]
+    static constexpr int kHdr = kWq + kCols * 128;           // [col C][16]
+    static constexpr int kWh = kHdr + kCols * 16;            // Q6K [col C][slot 4][16]
+    static constexpr int kWd = kWh + (kQ4K ? 0 : kCols * 64);  // Q6K [col C] dword (lanes past C repeat them)
     static constexpr int kAct = kWd + (kQ4K ? 0 : 64 * 4);   // [chunk 8][half 2][row 16][16]
     static constexpr int kBs = kAct + 8 * 2 * 16 * 16;       // Q4K [row 16][part 2][16]
     static constexpr int kDa = kBs + (kQ4K ? 16 * 32 : 0);   // [64] f32
     static constexpr int kSlot = kDa + 64 * 4;
-    // DMA instructions per super-block: weights, header (two dword DMAs),
-    // (Q6K: high bits, d), activation, (Q4K: bsums, two dword DMAs), d_a
-    static constexpr int kD = kQ4K ? 4 + 2 + 4 + 2 + 1 : 4 + 2 + 2 + 1 + 4 + 1;
+    // DMA instructions per super-block: weights (2 per 16 columns), header
+    // (one dword DMA per 16 columns), (Q6K: high bits, one per 16 columns,
+    // and d), activation, (Q4K: bsums, two dword DMAs), d_a
+    static constexpr int kD = kQ4K ? 3 * TC + 4 + 2 + 1 : 3 * TC + TC + 1 + 4 + 1;
 };
 
-template <int DT, int NW, int D>
+template <int DT, int NW, int D, int TC>
 __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, AView a, uint32_t m) {
-    using L = WkLay<DT>;
+    using L = WkLay<DT, TC>;
     constexpr bool kQ4K = L::kQ4K;
     static_assert((D - 2) * L::kD < 64, "vmcnt range");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -609,21 +610,22 @@ __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, A
     const uint32_t cmax = w.n - 1, rmax = m - 1;
 
     // per-lane DMA offsets (lanes past the last column or row re-read the last one)
-    uint32_t oq[4];
+    uint32_t oq[2 * TC];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 2 * TC; j++) {
         const uint32_t cl = 8 * j + (lane >> 3);
         oq[j] = min(col0 + cl, cmax) * w.q_row + ((lane & 7) ^ (cl & 7)) * 16;
     }
-    // headers: dword lane & 3 of column 16 j + lane / 4 (two dword DMAs, j = 0, 1);
-    // Q6K d: column lane & 31 (lanes 32..63 repeat columns 0..31 into the
-    // second half of the 256-byte region)
-    const uint32_t os0 = kq_tile_off(w.nb, min(col0 + (lane >> 2), cmax), 0, 16) + (lane & 3) * 4;
-    const uint32_t os1 = kq_tile_off(w.nb, min(col0 + 16 + (lane >> 2), cmax), 0, 16) + (lane & 3) * 4;
-    const uint32_t od = kq_tile_off((w.nb + 1) / 2, min(col0 + (lane & 31), cmax), 0, 4);
-    uint32_t oh[2];
+    // headers: dword lane & 3 of column 16 j + lane / 4 (one dword DMA per 16
+    // columns); Q6K d: column lane % C (lanes past C repeat the columns into
+    // the rest of the 256-byte region)
+    uint32_t os[TC];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < TC; j++) os[j] = kq_tile_off(w.nb, min(col0 + 16 * j + (lane >> 2), cmax), 0, 16) + (lane & 3) * 4;
+    const uint32_t od = kq_tile_off((w.nb + 1) / 2, min(col0 + (lane % (uint32_t)L::kCols), cmax), 0, 4);
+    uint32_t oh[TC];
+#pragma unroll
+    for (int j = 0; j < TC; j++) {
         const uint32_t cl = 16 * j + (lane >> 2);
         oh[j] = kQ4K ? 0u : min(col0 + cl, cmax) * w.h_row + ((lane & 3) ^ (cl & 3)) * 16;
     }
@@ -642,12 +644,12 @@ __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, A
         const uint32_t sb = wave + i * NW;
         const uint32_t slot = lbase + (i % D) * L::kSlot;
 #pragma unroll
-        for (int j = 0; j < 4; j++) dma16(w.q + sb * 128, oq[j], slot + L::kWq + 8 * j * 128);
-        dma4(w.st + sb * 16 * 128, os0, slot + L::kHdr);
-        dma4(w.st + sb * 16 * 128, os1, slot + L::kHdr + 256);
+        for (int j = 0; j < 2 * TC; j++) dma16(w.q + sb * 128, oq[j], slot + L::kWq + 8 * j * 128);
+#pragma unroll
+        for (int j = 0; j < TC; j++) dma4(w.st + sb * 16 * 128, os[j], slot + L::kHdr + 256 * j);
         if (!kQ4K) {
 #pragma unroll
-            for (int j = 0; j < 2; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + 16 * j * 64);
+            for (int j = 0; j < TC; j++) dma16(w.h + sb * 64, oh[j], slot + L::kWh + 16 * j * 64);
             dma4(w.dt + (sb >> 1) * 512, od, slot + L::kWd);
         }
 #pragma unroll
@@ -659,7 +661,9 @@ __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, A
         dma4(a.img + sb * 4, oda, slot + L::kDa);
     };
 
-    v4f acc[2] = {v4f{}, v4f{}};
+    v4f acc[TC];
+#pragma unroll
+    for (int ct = 0; ct < TC; ct++) acc[ct] = v4f{};
 #pragma unroll
     for (int i = 0; i < D - 1; i++)
         if ((uint32_t)i < nsb) issue(i);
@@ -669,8 +673,8 @@ __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, A
         // LDS reads have all been consumed; the asm barrier of the DMA keeps
         // them ahead of it
         if (i + D - 1 < nsb) issue(i + D - 1);
-        compute16<DT, L>(lds + (lbase - (uint32_t)(uintptr_t)lds) + (i % D) * L::kSlot, 0, lane,
-                         ((wave + i * NW) & 1) != 0, acc);
+        compute16<DT, L, TC>(lds + (lbase - (uint32_t)(uintptr_t)lds) + (i % D) * L::kSlot, 0, lane,
+                             ((wave + i * NW) & 1) != 0, acc);
     }
 
     // the wavefronts' sums, added in wavefront order
@@ -678,18 +682,19 @@ __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, A
     float* red = reinterpret_cast<float*>(lds);
     if (wave > 0) {
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++)
-            *reinterpret_cast<v4f*>(red + (((wave - 1) * 2 + ct) * 64 + lane) * 4) = acc[ct];
+        for (int ct = 0; ct < TC; ct++)
+            *reinterpret_cast<v4f*>(red + (((wave - 1) * TC + ct) * 64 + lane) * 4) = acc[ct];
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
     for (uint32_t v = 1; v < (uint32_t)NW; v++)
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++) acc[ct] += *reinterpret_cast<const v4f*>(red + (((v - 1) * 2 + ct) * 64 + lane) * 4);
+        for (int ct = 0; ct < TC; ct++)
+            acc[ct] += *reinterpret_cast<const v4f*>(red + (((v - 1) * TC + ct) * 64 + lane) * 4);
     const uint32_t g = lane >> 4;
 #pragma unroll
-    for (int ct = 0; ct < 2; ct++) {
+    for (int ct = 0; ct < TC; ct++) {
         const uint32_t col = col0 + ct * 16 + (lane & 15);
         if (col < w.n) {
 #pragma unroll
@@ -701,16 +706,15 @@ __global__ __launch_bounds__(64 * NW) void skinny_wk_kernel(WGroup G, SkOut O, A
     }
 }
 
-
-template <int DT, int NW, int D>
+template <int DT, int NW, int D, int TC>
 hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* partial, bool silu, hipStream_t s,
                             const ALayout* next, void* next_img) {
-    using L = WkLay<DT>;
+    using L = WkLay<DT, TC>;
     constexpr uint32_t kLds = (uint32_t)(NW * D * L::kSlot);
     static_assert(kLds <= 160 * 1024, "LDS budget");
-    static_assert(NW * D * L::kSlot >= (NW - 1) * 2 * 64 * 16, "reduction area");
+    static_assert(NW * D * L::kSlot >= (NW - 1) * TC * 64 * 16, "reduction area");
     {
-        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(skinny_wk_kernel<DT, NW, D>), kLds);
+        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(skinny_wk_kernel<DT, NW, D, TC>), kLds);
         if (e != hipSuccess) return e;
     }
     SkOut O{};
@@ -728,7 +732,7 @@ hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* pa
         off += cnt;
     }
     S.count = G.count;
-    hipLaunchKernelGGL((skinny_wk_kernel<DT, NW, D>), dim3(tiles), dim3(64 * NW), kLds, s, G, O, a, (uint32_t)m);
+    hipLaunchKernelGGL((skinny_wk_kernel<DT, NW, D, TC>), dim3(tiles), dim3(64 * NW), kLds, s, G, O, a, (uint32_t)m);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !silu) return e;
     if (next) return launch_sum_silu_quant(S, 1, m, G.w[0].n, *next, next_img, s);
@@ -745,6 +749,13 @@ hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* pa
 // 4096 Q4_K 19.4 -> 22.3, Q6_K 24.7 -> 32.3) and more tiles take extra
 // rounds (the gate/up pair 25.5 -> 29.9, the Q6_K lm_head 125 -> 164).
 // XNQ_SKINNY_WK=0 turns it off, 2 forces it for every 16-row launch (tuning).
+// One 16-column tile per wavefront (twice the workgroups, a 7-8 KB slot)
+// where the 32-column form leaves CUs idle or, for Q6_K, fits only one
+// workgroup per CU (graph steps at m = 16, µs, two tiles -> one): Q4_K 4096 x
+// 4096 (128 column tiles of 32) 11.2 -> 9.7; Q6_K 1792 -> 4096 10.2 -> 8.3,
+// 4096 x 4096 14.2 -> 10.6, 4096 -> 14336 24.9 -> 23.1; the Q4_K q/k/v group
+// (192 tiles) 11.7 -> 13.0 and 4096 -> 14336 16.8 -> 19.9 keep two.
+static bool wk_one_tile(uint32_t dtype, size_t tiles32) { return dtype == XNQ_Q6K || tiles32 <= 128; }
 static bool skinny_wk(uint32_t dtype, size_t tiles32, size_t k) {
     static const int mode = [] {
         const char* e = getenv("XNQ_SKINNY_WK");
@@ -857,7 +868,7 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
 #define XNQ_SK(DT)                                                                                   \
     if (G.w[0].dtype == DT) {                                                                        \
         if (m <= 16 && skinny16() && skinny_wk(DT, tiles32, G.w[0].k) && (!silu || partial))       \
-            return launch_skinny_wk<DT, 4, 2>(G, a, m, partial, silu, s, next, next_img);             \
+            return wk_one_tile(DT, tiles32) ? launch_skinny_wk<DT, 4, 2, 1>(G, a, m, partial, silu, s, next, next_img) : launch_skinny_wk<DT, 4, 2, 2>(G, a, m, partial, silu, s, next, next_img); \
         if (m <= 16 && skinny16())                                                                 \
             return w8 ? launch_skinny_dt<DT, 0, 8>(G, a, m, splits, partial, silu, s, next, next_img)               \
                       : launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s, next, next_img);              \
