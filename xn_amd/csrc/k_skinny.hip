@@ -739,16 +739,6 @@ hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* pa
     return launch_sum_group(S, 1, true, s);
 }
 
-// The wavefront-split kernel where it measured faster than the split-K one
-// plus its sum launch (graph steps at m = 16, µs): K <= 4096 and at most 512
-// column tiles of 32, which two workgroups per CU (Q4_K) or one round and a
-// half (Q6_K) cover: Q4_K 4096 x 4096 13.4 -> 11.4, the q/k/v group 15.0 ->
-// 12.1, 4096 -> 14336 18.3 -> 16.7; Q6_K 1792 -> 4096 14.8 -> 10.5, 2048 ->
-// 8192 15.1 -> 11.8, 4096 -> 14336 26.1 -> 25.7; batch-16 decode step 2520
-// -> 2376.  Longer K leaves each wavefront a long serial chain (14336 ->
-// 4096 Q4_K 19.4 -> 22.3, Q6_K 24.7 -> 32.3) and more tiles take extra
-// rounds (the gate/up pair 25.5 -> 29.9, the Q6_K lm_head 125 -> 164).
-// XNQ_SKINNY_WK=0 turns it off, 2 forces it for every 16-row launch (tuning).
 // One 16-column tile per wavefront (twice the workgroups, a 7-8 KB slot)
 // where the 32-column form leaves CUs idle or, for Q6_K, fits only one
 // workgroup per CU (graph steps at m = 16, µs, two tiles -> one): Q4_K 4096 x
@@ -756,14 +746,30 @@ hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* pa
 // 4096 x 4096 14.2 -> 10.6, 4096 -> 14336 24.9 -> 23.1; the Q4_K q/k/v group
 // (192 tiles) 11.7 -> 13.0 and 4096 -> 14336 16.8 -> 19.9 keep two.
 static bool wk_one_tile(uint32_t dtype, size_t tiles32) { return dtype == XNQ_Q6K || tiles32 <= 128; }
+
+// The wavefront-split kernel where it measured faster than the split-K one
+// plus its sum launch (graph steps at m = 16, µs): at most 512 column tiles
+// of 32, and K <= 4096 unless the one-tile form's workgroups fit one round
+// at two per CU.  Q4_K 4096 x 4096 13.4 -> 9.7, the q/k/v group 15.0 ->
+// 11.7, 4096 -> 14336 18.3 -> 16.8, 14336 -> 4096 18.9 -> 18.2; Q6_K 1792 ->
+// 4096 14.8 -> 8.3, 14336 -> 4096 25.3 -> 21.0.  With two tiles per
+// wavefront, K = 14336 was slower (Q4_K 14336 -> 4096 19.4 -> 22.3: half the
+// CUs, 14 super-blocks per wavefront), and so are more tiles, which take
+// extra rounds (the gate/up pair 25.5 -> 29.9, 8192 -> 28672 40.1 -> 44.2,
+// the Q6_K lm_head 125 -> 164).  XNQ_SKINNY_WK=0 turns it off, 2 forces it
+// for every 16-row launch (tuning).
 static bool skinny_wk(uint32_t dtype, size_t tiles32, size_t k) {
     static const int mode = [] {
         const char* e = getenv("XNQ_SKINNY_WK");
         return e ? atoi(e) : 1;
     }();
     if (mode == 2) return true;
-    (void)dtype;
-    return mode != 0 && k <= 4096 && tiles32 <= 512;
+    if (mode == 0 || tiles32 > 512) return false;
+    // the one-tile form at any K while its workgroups fit one round at two
+    // per CU (Q6_K 14336 -> 4096, 128 tiles: 25.3 -> 21.0 µs; Q4_K
+    // 14336 -> 4096 18.9 -> 18.2), else K <= 4096
+    if (wk_one_tile(dtype, tiles32) && 2 * tiles32 <= 512) return true;
+    return k <= 4096;
 }
 
 template <int DT, int MT, int NW>
