@@ -163,8 +163,8 @@ def test_matmul_small(orc, dev, dt, m, entry):
     (Q4K, 4096, 1792),    # an 8-way column-parallel shard of gate/up
     (Q6K, 1792, 4096),    # an 8-way row-parallel shard of down
 ])
-# m = 5 and 8: the skinny kernel for Q4_K / Q6_K with N or K >= 8192, the
-# matvec for 4096 x 4096, the shards and the other dtypes
+# m = 4: the matvec; m = 5 and 8: the skinny kernel for Q4_K / Q6_K, the
+# matvec for the other dtypes
 @pytest.mark.parametrize("m", [1, 4, 5, 8])
 def test_matmul_config_shapes(orc, dev, dt, k, n, m):
     rng = np.random.default_rng(7000 + dt + k + n + m)
@@ -328,8 +328,8 @@ def test_matmul_group(orc, dev, dt, m, ns):
 @pytest.mark.parametrize("m", [2, 3, 5])
 def test_group_decode_shapes(orc, dev, m):
     """q/k/v (4096 -> 4096, 1024, 1024) and the gate/up pair (4096 -> 14336)
-    of config 5 at few rows: one joined skinny launch from m = 3, the
-    matvec at m = 2."""
+    of config 5 at few rows: q/k/v as one joined skinny launch from m = 2,
+    the gate/up pair from m = 3 (the matvec at m = 2)."""
     from xn_amd.quantized import matmul_t_group, matmul_t_silu_gate
 
     k = 4096

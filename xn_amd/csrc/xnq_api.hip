@@ -432,16 +432,17 @@ static xnq_status check_mkn(const xnq_qtensor* qt, size_t m, size_t k, size_t n)
 }
 
 // Automatic routes (measured on MI355X):
-//   m <= 8 matvec kernels (up to 8 rows per launch), except where the skinny
-//     kernel is faster: from m = 5 on Q4K / Q6K weights with n >= 8192 or
-//     k >= 8192, from m = 3 for a group of weights sharing one activation
-//     (q/k/v, gate/up) that joins at least 6144 columns
+//   m <= 4   matvec kernels (up to 8 rows per launch), except a group of
+//            weights sharing one activation (q/k/v, gate/up) that joins at
+//            least 6144 columns: skinny from m = 3, or from m = 2 when the
+//            group joins at most 16384 columns (the wavefront-split kernel)
 //   m <= 64  skinny int8-MFMA kernel for Q4K / Q6K
 //   larger m tiled int8-MFMA prefill kernel
-// Q8_0 / Q4_0 always take the matvec kernels.  XNQ_SKINNY_MIN_ROWS and
-// XNQ_SKINNY_MAX_ROWS override the skinny range for tuning (read once per
-// process); `forced` is xnq_set_route's override as read at the entry point;
-// `group_n` is the joined width of a group (0 for a single weight).
+// Q8_0 / Q4_0 and the other dtypes always take the matvec kernels.
+// XNQ_SKINNY_MIN_ROWS and XNQ_SKINNY_MAX_ROWS override the skinny range for
+// tuning (read once per process); `forced` is xnq_set_route's override as
+// read at the entry point; `group_n` is the joined width of a group (0 for a
+// single weight).
 enum Route { kMatvec, kSkinny, kMfma };
 
 static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced, size_t group_n = 0) {
@@ -453,16 +454,16 @@ static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced
     // measured crossovers (graph steps, µs, matvec against skinny): the
     // matvec kernels' cost jumps from 4 to 5 rows (the 8-row template) and
     // past 8 rows takes a second launch; the skinny kernel's hardly grows
-    // below 32 rows.  4096 -> 14336 Q4_K at m = 5: 18.9 against 17.5;
-    // 14336 -> 4096 Q4_K 25.5 against 18.8, Q6_K 26.3 against 24.3;
-    // 4096 -> 128256 Q6_K 186 against 119; 4096 x 4096 at m = 8 10.7
-    // against 13.2 (matvec up to 8 rows).  Groups: gate/up pair at m = 3
-    // 28.5 against 24.6, q/k/v 18.0 against 14.0; at m = 2 the matvec wins
-    // (22.1 against 25.5, 13.5 against 14.2).
-    const size_t skinny_lo = skinny_min                      ? skinny_min
-                             : group_n >= 6144               ? 3
-                             : n >= 8192 || k >= 8192        ? 5
-                                                             : 9;
+    // below 32 rows.  At m = 5: 4096 x 4096 10.5 against 9.2, 4096 -> 14336
+    // 13.9 against 13.9, 4096 -> 1792 8.7 / 8.5, Q6_K 1792 -> 4096 8.8 / 8.2,
+    // Q6_K 4096 x 4096 11.7 / 10.2, 2048 x 2048 7.4 / 6.6; at m = 3 the
+    // matvec wins (7.3 / 8.4, 6.7 / 7.7, 8.7 / 10.2, 33.9 / 37.4 on
+    // 8192 -> 28672).  Groups: q/k/v at m = 2 13.4 against 10.6; the gate/up
+    // pair at m = 2 22.2 against 24.5, at m = 3 24.0 / 24.1.
+    const size_t skinny_lo = skinny_min            ? skinny_min
+                             : group_n > 16384     ? 3
+                             : group_n >= 6144     ? 2
+                                                   : 5;
     if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
     if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
     return kMatvec;
