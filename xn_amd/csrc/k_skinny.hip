@@ -812,33 +812,40 @@ hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t 
 
 }  // namespace
 
-// Wavefronts per workgroup (32 columns each): 8 (two per SIMD, so one
-// wavefront's expansion overlaps the other's waits) above 32 rows (two row
-// tiles: 4096 x 4096 at m = 64 13.8 against 16.2 us) or where the column
-// tiles still cover the CUs with K split at most 4 ways, else 4.
-// XNQ_SKINNY_NW=4|8 forces it (tuning).
+// Wavefronts per workgroup (32 columns each): 4 for the 16-row tiles (m <=
+// 16), whose 47 KB workgroups fit three to a CU (8192 -> 28672 at m = 16
+// 40.2 against 45.6 us with 8 at the same split count, 37.9 with twice the
+// splits); above, 8 (two per SIMD, so one wavefront's expansion overlaps the
+// other's waits) above 32 rows (two row tiles: 4096 x 4096 at m = 64 13.8
+// against 16.2 us) or where the column tiles still cover the CUs with K
+// split at most 4 ways, else 4.  XNQ_SKINNY_NW=4|8 forces it (tuning).
 static int skinny_waves(size_t m, size_t n, size_t k) {
     static const int forced = [] {
         const char* e = getenv("XNQ_SKINNY_NW");
         return e ? atoi(e) : 0;
     }();
     if (forced == 4 || forced == 8) return forced;
+    if (m <= 16) return 4;
     if (m > 32) return 8;
     const size_t tiles8 = (n + 255) / 256, nsb = k / 256;
     return tiles8 * std::min<size_t>(4, nsb / 2) >= 200 ? 8 : 4;
 }
 
 uint32_t skinny_splits(size_t m, size_t n, size_t k) {
-    // split K while the grid still has about one workgroup per CU, each split
-    // at least two super-blocks long (more splits, for two or three
-    // workgroups per CU, measured slower: batch-16 decode step 2514 us at
-    // 256, 2715 at 512; XNQ_SKINNY_WG_TARGET overrides the 256, tuning)
+    // split K while the grid has about one workgroup per CU (16-row tiles:
+    // two, which fit three to a CU), each split at least two super-blocks
+    // long.  The 16-row split-K launches that remain (those the
+    // wavefront-split kernel does not take: many column tiles) gained from
+    // the second workgroup per CU (8192 -> 28672 at m = 16 40.2 -> 37.9 us,
+    // the Q6_K lm_head 116 -> 111); the 32-row tiles keep one.
+    // XNQ_SKINNY_WG_TARGET overrides the target (tuning).
     const size_t tiles = (n + 32 * skinny_waves(m, n, k) - 1) / (32 * skinny_waves(m, n, k));
     const size_t nsb = k / 256;
-    static const size_t target = [] {
+    static const size_t forced_target = [] {
         const char* e = getenv("XNQ_SKINNY_WG_TARGET");
-        return e && atoi(e) > 0 ? (size_t)atoi(e) : (size_t)256;
+        return e && atoi(e) > 0 ? (size_t)atoi(e) : (size_t)0;
     }();
+    const size_t target = forced_target ? forced_target : m <= 16 ? 512 : 256;
     size_t splits = target / tiles;
     if (splits > nsb / 2) splits = nsb / 2;
     return splits < 1 ? 1u : (uint32_t)splits;
