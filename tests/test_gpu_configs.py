@@ -132,8 +132,9 @@ def test_config2_q4_0_ffn_block(checker, weights, dev, fused):
 # ------------------------------------------------------------ config 3
 @pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 28672)])
 def test_config3_q4k_sweep(checker, weights, dev, k, n):
-    """Q4_K matvec sweep at M = 1, 2, 4, 8 (matvec, and skinny where the
-    route table sends it: m >= 6 at N >= 8192, m = 8 at K >= 8192)."""
+    """Q4_K matvec sweep at M = 1, 2, 4, 8 (the matvec up to m = 4, the
+    skinny kernel at m = 8: the wavefront-split form where it applies,
+    split-K on 8192 -> 28672)."""
     qt, blocks = weights.get(Q4K, n, k)
     for m in (1, 2, 4, 8):
         x = x_rows(m, k, SEED + m + k)
