@@ -747,11 +747,13 @@ hipError_t launch_skinny_wk(const WGroup& G, const AView& a, size_t m, float* pa
 // (192 tiles) 11.7 -> 13.0 and 4096 -> 14336 16.8 -> 19.9 keep two.
 static bool wk_one_tile(uint32_t dtype, size_t tiles32) { return dtype == XNQ_Q6K || tiles32 <= 128; }
 // Eight wavefronts (half the serial chain each, one workgroup per CU) for
-// the one-tile form at K > 4096 and up to 8 rows (graph steps, µs, four ->
-// eight: 14336 -> 4096 Q4_K at m = 5 17.9 -> 14.4, m = 8 17.2 -> 15.4; Q6_K
-// 20.6 -> 19.7, 20.1 -> 18.6; at m = 12 a tie, at m = 16 18.0 -> 18.6 and
-// 20.1 -> 21.6).
-static bool wk_eight_waves(uint32_t k, size_t m) { return k > 4096 && m <= 8; }
+// the one-tile form up to 8 rows when its workgroups fit on the CUs one each
+// (graph steps, µs, four -> eight): 14336 -> 4096 Q4_K at m = 5 17.9 -> 14.4,
+// m = 8 17.2 -> 15.4; Q6_K 20.6 -> 19.7, 20.1 -> 18.6; 4096 x 4096 Q4_K at
+// m = 5 9.4 -> 8.4, Q6_K 10.2 -> 9.8; 4096 -> 1792 8.5 -> 7.6.  More
+// workgroups than CUs lose (Q6_K 2048 -> 8192 9.9 -> 11.8, 4096 -> 14336
+// 20.5 -> 24.7), and so do more rows (m = 16: 18.0 -> 18.6, 20.1 -> 21.6).
+static bool wk_eight_waves(size_t tiles32, size_t m) { return m <= 8 && 2 * tiles32 <= 256; }
 
 // The wavefront-split kernel where it measured faster than the split-K one
 // plus its sum launch (graph steps at m = 16, µs): at most 512 column tiles
@@ -888,7 +890,7 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
     if (G.w[0].dtype == DT) {                                                                        \
         if (m <= 16 && skinny16() && skinny_wk(DT, tiles32, G.w[0].k) && (!silu || partial))       \
             return wk_one_tile(DT, tiles32)                                                          \
-                       ? (wk_eight_waves(G.w[0].k, m)                                                 \
+                       ? (wk_eight_waves(tiles32, m)                                                  \
                               ? launch_skinny_wk<DT, 8, 2, 1>(G, a, m, partial, silu, s, next, next_img) \
                               : launch_skinny_wk<DT, 4, 2, 1>(G, a, m, partial, silu, s, next, next_img)) \
                        : launch_skinny_wk<DT, 4, 2, 2>(G, a, m, partial, silu, s, next, next_img);     \
