@@ -309,6 +309,7 @@ def test_silu_gate(orc, dev, dt, m, k, n):
 
 @pytest.mark.parametrize("dt", WEIGHT_DTYPES)
 @pytest.mark.parametrize("m,ns", [(1, (300,)), (1, (512, 128, 128)), (1, (40, 7)), (2, (200, 64, 64)),
+                                  (5, (300, 96, 40)), (8, (512, 128, 128)),
                                   (16, (512, 128, 128)), (16, (200, 72, 40)), (40, (300, 96)), (80, (256, 64))])
 def test_matmul_group(orc, dev, dt, m, ns):
     """q, k, v projections of one activation (llama.rs:156-158) in one launch."""
