@@ -102,8 +102,9 @@ size_t xnq_qtensor_device_bytes(const xnq_qtensor* qt);
 /* dst[m x n] = lhs[m x k] . W^T, with lhs quantized to the weight's vec-dot
  * type first.  Replaces QTensor::matmul_t / QuantizedType::matmul_t /
  * k_quants::matmul (mod.rs:334-339, 221-223; k_quants.rs:1996-2011).  The
- * route is chosen from m: a wavefront-per-row matvec for small m, an int8
- * MFMA kernel for prefill-sized m.  Validates what xn validates:
+ * route is chosen from m: a wavefront-per-row matvec for small m (Q4_K /
+ * Q6_K up to 4 rows), the small-batch int8 MFMA kernel up to 64 rows, the
+ * tiled int8 MFMA kernel for prefill-sized m.  Validates what xn validates:
  * mkn against the weight shape (repack.rs:203-215) and m*k == lhs length is
  * the caller's contract.  Stream ordered; allocates its activation scratch
  * stream-ordered (hipMallocAsync). */
@@ -146,16 +147,18 @@ xnq_status xnq_qtensor_matmul_t_noalloc(const xnq_qtensor* qt, size_t m, size_t 
  * (cpu_backend.rs:354-356); gate and up have one shape.  m == 1 with both on
  * the one-launch route (K <= 4096 at any N, or weights of up to 6144 x 4096
  * elements) and K <= 10240 is one kernel and needs no workspace; on the
- * small-batch MFMA route (Q4_K/Q6_K, 12 <= m <= 64) one quantize, one
- * launch over both weights and one split-sum that applies the SiLU-multiply;
+ * small-batch MFMA route (Q4_K/Q6_K, 3 <= m <= 64 for the 4096 -> 14336
+ * pair) one quantize, one launch over both weights and one split-sum that
+ * applies the SiLU-multiply;
  * otherwise one activation quantize serves both products (matmul_preq
  * each), then a SiLU-multiply kernel, with workspace for the second product.
  *
  * group: dsts[i][m x n_i] = lhs . qts[i]^T for up to 3 weights of one dtype
  * and K (the q, k, v projections of llama.rs:156-158); m == 1 on the
  * one-launch route is one kernel over the joined rows; on the small-batch
- * MFMA route one quantize, one launch over the joined column tiles and one
- * split-sum; otherwise weights of one dtype and K share one activation
+ * MFMA route (from m = 2 for a q/k/v-sized group) one quantize and one
+ * launch over the joined column tiles, plus a split-sum where K is split
+ * across workgroups; otherwise weights of one dtype and K share one activation
  * quantize (matmul_preq each), and other groups take one matmul_t_ws per
  * weight.  Workspace sizes are 0 when the
  * single-kernel route applies. */
