@@ -224,11 +224,14 @@ def test_matmul_q4k_multirow_matvec(orc, dev, m, n, k):
 
 
 @pytest.mark.parametrize("dt", [Q4K, Q6K])
-@pytest.mark.parametrize("m,n,k", [(2, 300, 2048), (5, 129, 768), (8, 512, 4096), (16, 200, 1024),
-                                   (31, 384, 2304), (33, 256, 1280), (64, 130, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 300, 2048), (2, 300, 2048), (5, 129, 768), (7, 40, 256), (8, 512, 4096),
+                                   (8, 100, 8192), (16, 200, 1024), (31, 384, 2304), (33, 256, 1280),
+                                   (64, 130, 512)])
 def test_matmul_skinny(orc, dev, dt, m, n, k):
-    """The skinny int8-MFMA route (forced) for 2 <= m <= 64: one and two 32-row
-    tiles, ragged n against the 128-column workgroups, split-K."""
+    """The skinny int8-MFMA route (forced) for 1 <= m <= 64: 16-row tiles (K
+    split across a workgroup's wavefronts, with fewer super-blocks than
+    wavefronts at K = 256 and eight wavefronts at K = 8192), one and two
+    32-row tiles, ragged n against the column tiles, split-K."""
     from xn_amd.quantized import set_route
 
     rng = np.random.default_rng(8500 + dt + m + n + k)
