@@ -123,22 +123,24 @@ hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hip
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s) {
+hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s,
+                               bool one_shot) {
+    const int fused = one_shot ? kFusedOneShot : kFusedPersistent;
     AView a{};
     a.k = w.k;
     a.m = (uint32_t)m;
     a.A = act_img(w.k, is_kquant(w.dtype));
     switch (w.dtype) {
-    case XNQ_Q8_0: return launch_matvec_q8_0(w, a, x, m, y, s, true);
-    case XNQ_Q4_0: return launch_matvec_q4_0(w, a, x, m, y, s, true);
-    case XNQ_Q4K: return launch_matvec_q4k(w, a, x, m, y, s, true);
-    case XNQ_Q6K: return launch_matvec_q6k(w, a, x, m, y, s, true);
-    case XNQ_Q4_1: return launch_matvec_q4_1(w, a, x, m, y, s, true);
-    case XNQ_Q5_0: return launch_matvec_q5_0(w, a, x, m, y, s, true);
-    case XNQ_Q5_1: return launch_matvec_q5_1(w, a, x, m, y, s, true);
-    case XNQ_Q2K: return launch_matvec_q2k(w, a, x, m, y, s, true);
-    case XNQ_Q3K: return launch_matvec_q3k(w, a, x, m, y, s, true);
-    case XNQ_Q5K: return launch_matvec_q5k(w, a, x, m, y, s, true);
+    case XNQ_Q8_0: return launch_matvec_q8_0(w, a, x, m, y, s, fused);
+    case XNQ_Q4_0: return launch_matvec_q4_0(w, a, x, m, y, s, fused);
+    case XNQ_Q4K: return launch_matvec_q4k(w, a, x, m, y, s, fused);
+    case XNQ_Q6K: return launch_matvec_q6k(w, a, x, m, y, s, fused);
+    case XNQ_Q4_1: return launch_matvec_q4_1(w, a, x, m, y, s, fused);
+    case XNQ_Q5_0: return launch_matvec_q5_0(w, a, x, m, y, s, fused);
+    case XNQ_Q5_1: return launch_matvec_q5_1(w, a, x, m, y, s, fused);
+    case XNQ_Q2K: return launch_matvec_q2k(w, a, x, m, y, s, fused);
+    case XNQ_Q3K: return launch_matvec_q3k(w, a, x, m, y, s, fused);
+    case XNQ_Q5K: return launch_matvec_q5k(w, a, x, m, y, s, fused);
     }
     return hipErrorInvalidValue;
 }

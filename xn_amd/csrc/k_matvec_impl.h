@@ -590,7 +590,9 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     // whole first row group; the activation image is built while the weight
     // loads travel.
     StagePrefetch<MB, NW> pre;
-    XQuant<DT, MB, NW, 4> xq;
+    // one round of the fused quantizer covers 4096 elements of a row per
+    // 4 * 4 / NW blocks per wavefront (further rounds in xq.rest)
+    XQuant<DT, MB, NW, (NW >= 16 ? 1 : NW >= 8 ? 2 : 4)> xq;
     if (FUSED) xq.load(x, w.k, m0, mcount, xq.first(wave), lane);
     else pre.load(a, m0, mcount);
     issue(min(g, ngroups - 1), 0);
@@ -934,12 +936,14 @@ inline int pick_rows(uint32_t n, int cpl) {
     return 1;
 }
 
-// y[m x n] for all m rows, in launches of up to 8 rows: `fused` quantizes
-// each launch's rows from f32 `x` in LDS, else the kernels read the Q8
-// workspace `a`.
+// y[m x n] for all m rows, in launches of up to 8 rows: `fused` nonzero
+// quantizes each launch's rows from f32 `x` in LDS (kFusedOneShot: at m == 1
+// the one-shot group kernel, one wavefront per row, for small weights; else
+// the persistent matvec kernel with 16-wavefront workgroups), zero reads the
+// Q8 workspace `a`.
 template <int DT>
 hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m, float* y,
-                        hipStream_t s, bool fused) {
+                        hipStream_t s, int fused) {
     constexpr bool kq = is_kquant(DT);
     int gmax = 8;
     while (gmax > 1 && lds_bytes(gmax, w.k, kq) > kMaxLds) gmax >>= 1;
@@ -949,7 +953,7 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
         const uint32_t mc = (uint32_t)((m - m0) < (size_t)gmax ? (m - m0) : (size_t)gmax);
         hipError_t e;
         static const bool legacy = env_int("XNQ_MV_LEGACY", 0) != 0;
-        if (mc == 1 && m == 1 && fused && !legacy) {
+        if (mc == 1 && m == 1 && fused == kFusedOneShot && !legacy) {
             WGroup g{};
             g.w[0] = w;
             g.y[0] = y;
@@ -980,16 +984,16 @@ hipError_t launch_group_dt(const WGroup& g, const float* x, bool gate, hipStream
     return gate ? mv::launch_group<DT, true>(g, x, s) : mv::launch_group<DT, false>(g, x, s);
 }
 
-hipError_t launch_matvec_q4_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q8_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q4k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q6k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q4_1(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q5_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q5_1(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q2k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q3k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
-hipError_t launch_matvec_q5k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, bool);
+hipError_t launch_matvec_q4_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q8_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q4k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q6k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q4_1(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q5_0(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q5_1(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q2k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q3k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
+hipError_t launch_matvec_q5k(const WView&, const AView&, const float*, size_t, float*, hipStream_t, int);
 hipError_t launch_group_q4_1(const WGroup&, const float*, bool, hipStream_t);
 hipError_t launch_group_q5_0(const WGroup&, const float*, bool, hipStream_t);
 hipError_t launch_group_q5_1(const WGroup&, const float*, bool, hipStream_t);

@@ -4,7 +4,7 @@
 namespace xnq {
 
 hipError_t launch_matvec_q2k(const WView& w, const AView& a, const float* x, size_t m, float* y, hipStream_t s,
-                            bool fused) {
+                            int fused) {
     return mv::launch_dtype<XNQ_Q2K>(w, a, x, m, y, s, fused);
 }
 

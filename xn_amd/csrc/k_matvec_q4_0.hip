@@ -4,7 +4,7 @@
 namespace xnq {
 
 hipError_t launch_matvec_q4_0(const WView& w, const AView& a, const float* x, size_t m, float* y,
-                           hipStream_t s, bool fused) {
+                           hipStream_t s, int fused) {
     return mv::launch_dtype<XNQ_Q4_0>(w, a, x, m, y, s, fused);
 }
 

@@ -530,35 +530,40 @@ xnq_status xnq_qtensor_matmul_preq(const xnq_qtensor* qt, size_t m, size_t k, si
 }
 
 // Decode: the fused matvec route quantizes the activation row in LDS inside
-// the matvec kernel and needs no workspace.  It saves the quantize launch
-// (~1.8 us), but every workgroup quantizes the whole row, so on large
-// weights it streams more slowly than quantize + matvec (measured at m = 1:
-// 4096 -> 14336: 9.6 against 9.45 us; 14336 -> 4096 Q6_K: 14.2 against 13.2;
-// 8192 -> 28672: 36.9 against 25.0) and with m (m = 2, 14336 -> 4096: 23 us
-// against 11 + 1.8).  A single matmul_t takes it for m = 1 on weights of up
-// to XNQ_FUSED_MAX_ELEMS (6144 x 4096) elements.  The q/k/v group and the
-// SiLU-gated gate/up pair take it whenever K <= XNQ_FUSED_MAX_K (4096): one
-// launch for several weights wins there (decode step 1540 -> 1432 us).
+// the matvec kernel and needs no workspace, which saves the quantize launch
+// (~1.8 us).  Every workgroup quantizes the whole row, so it pays only while
+// rows are short: m = 1 on weights of up to XNQ_FUSED_MAX_ELEMS (6144 x 4096)
+// elements, or rows of K <= XNQ_FUSED_MAX_K (4096) at any N; the q/k/v group
+// and the SiLU-gated gate/up pair take one launch for several weights there
+// (decode step 1540 -> 1432 us).  Longer rows and more activation rows take
+// quantize + matvec (14336 -> 4096 Q6_K: 19.6 fused against 12.8; m = 2,
+// 14336 -> 4096: 23 against 11 + 1.8).
 static size_t fused_max_elems() {
     static const size_t v = env_size("XNQ_FUSED_MAX_ELEMS", (size_t)6144 * 4096);
     return v;
 }
 
-// Rows of at most this K take the fused m = 1 kernel at any N.
 static size_t fused_max_k() {
     static const size_t v = env_size("XNQ_FUSED_MAX_K", 4096);
     return v;
 }
 
-// `grouped`: the weight is one of a q/k/v group or a gate/up pair, whose
-// one-launch kernels take K <= XNQ_FUSED_MAX_K at any N; a single matmul_t
-// takes the element limit alone.
-static bool fused_route(const xnq_qtensor* qt, size_t m, int forced, bool grouped = false) {
+// m == 1 takes one kernel that quantizes the row in LDS: weights of up to
+// XNQ_FUSED_MAX_ELEMS elements the one-shot group kernel (one wavefront per
+// row), rows of K <= XNQ_FUSED_MAX_K at any N (alone, or one of a q/k/v
+// group or a gate/up pair, whose one-launch kernels take them) the
+// persistent matvec kernel with 16-wavefront workgroups, each quantizing the
+// row once (graph steps against quantize + matvec, µs: Q4_K 4096 -> 14336
+// 9.3 against 9.7, Q4_0 4096 -> 14336 7.9 against 9.2, Q6_K 4096 -> 128256
+// 68.9 against 72.1; at K = 14336 quantizing 56 blocks per workgroup costs
+// more than the separate launch: 14336 -> 4096 Q6_K 19.6 against 12.8).
+static bool fused_route(const xnq_qtensor* qt, size_t m, int forced) {
     const Route r = pick_route(qt->L.dtype, m, qt->L.n, qt->L.k, forced);
     if (r != kMatvec) return false;
     if (forced == 1) return true;
-    return m == 1 && ((grouped && qt->L.k <= fused_max_k()) || qt->L.n * qt->L.k <= fused_max_elems());
+    return m == 1 && (qt->L.k <= fused_max_k() || qt->L.n * qt->L.k <= fused_max_elems());
 }
+static bool fused_one_shot(const xnq_qtensor* qt) { return qt->L.n * qt->L.k <= fused_max_elems(); }
 
 static size_t matmul_t_workspace_size_impl(const xnq_qtensor* qt, size_t m, int forced) {
     if (!qt || fused_route(qt, m, forced)) return 0;
@@ -583,7 +588,7 @@ static xnq_status matmul_t_ws_impl(const xnq_qtensor* qt, size_t m, size_t k, si
     hipStream_t s = (hipStream_t)stream;
     if (fused_route(qt, m, forced)) {
         const WView w = make_wview(qt->L, qt->buf);
-        hipError_t e = launch_matvec_fused(w, lhs_dev, m, dst_dev, s);
+        hipError_t e = launch_matvec_fused(w, lhs_dev, m, dst_dev, s, fused_one_shot(qt));
         if (e == hipErrorInvalidConfiguration)
             return fail(XNQ_ERR_INVALID, "k = %zu is too large for the matvec kernel's LDS", k);
         if (e != hipSuccess) return hip_fail(e, "matvec kernel");
@@ -687,7 +692,7 @@ xnq_status xnq_qtensor_matmul_t_noalloc(const xnq_qtensor* qt, size_t m, size_t 
 static bool group_route(const xnq_qtensor* const* qts, size_t count, size_t m, int forced) {
     if (m != 1 || count == 0 || count > (size_t)kMaxGroup) return false;
     for (size_t i = 0; i < count; i++) {
-        if (!qts[i] || !fused_route(qts[i], m, forced, true)) return false;
+        if (!qts[i] || !fused_route(qts[i], m, forced)) return false;
         if (qts[i]->L.dtype != qts[0]->L.dtype || qts[i]->L.k != qts[0]->L.k || qts[i]->device != qts[0]->device)
             return false;
     }

@@ -234,8 +234,12 @@ hipError_t launch_weight_from_float(uint32_t dtype, size_t nblocks, const float*
                                     hipStream_t s);
 // k_matvec.hip
 hipError_t launch_matvec(const WView& w, const AView& a, size_t m, float* y, hipStream_t s);
-// m == 1: quantizes the f32 row inside the kernel (no workspace).
-hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s);
+// Quantizes the f32 rows inside the kernel (no workspace).  `one_shot`: at
+// m == 1 the one-shot group kernel (one wavefront per weight row; small
+// weights), else the persistent matvec kernel.
+constexpr int kFusedPersistent = 1, kFusedOneShot = 2;
+hipError_t launch_matvec_fused(const WView& w, const float* x, size_t m, float* y, hipStream_t s,
+                               bool one_shot);
 // m == 1 over a weight group (gate: silu(x . w0) * (x . w1)); hipErrorNotSupported
 // for a shape the grouped kernel does not take
 hipError_t launch_matvec_group(const WGroup& g, const float* x, bool gate, hipStream_t s);
