@@ -651,11 +651,13 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
 //   GATE: two weights of the same shape (gate, up), one output
 //     y = silu(x . gate) * (x . up), the SwiGLU of llama.rs:258-264 with
 //     silu(s) = s / (1 + exp(0 - s)) (cpu_backend.rs:354-356).
-// Every wavefront owns R rows (GATE: R rows of each weight) and there is no
-// grid-stride loop, so the kernel is straight-line code: the activation
-// loads, then every weight load of the wavefront's rows (K <= 64 * CPL * 32;
-// longer rows take further passes), then the activation image is built in
-// LDS while the weight stream is in flight.
+// Every wavefront owns R rows at a time (GATE: R rows of each weight): the
+// activation loads, then every weight load of the wavefront's rows (K <= 64 *
+// CPL * 32; longer rows take further passes), then the activation image is
+// built in LDS while the weight stream is in flight.  The grid is capped at
+// the workgroups resident at once; past that the wavefronts stride over the
+// remaining row groups, each group's loads issued before the previous
+// group's reduction.
 template <int DT, int R, int CPL, int NW, bool GATE>
 __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* __restrict__ x) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -671,7 +673,11 @@ __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* _
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t nchunks = k / 32;
     const uint32_t npass = (nchunks + 64 * CPL - 1) / (64 * CPL);
-    const uint32_t row0 = (blockIdx.x * NW + wave) * R;
+    // row groups of R rows, grid-strided when the grid is smaller than the
+    // group count (the launch caps it at the workgroups resident at once)
+    const uint32_t ngroups = (G.rows + R - 1) / R, gstride = gridDim.x * NW;
+    uint32_t grp = blockIdx.x * NW + wave;
+    uint32_t row0 = grp * R;
 
     // weight t and local row of loaded row r (wavefront-uniform)
     auto locate = [&](int r, uint32_t& t, uint32_t& lr) {
@@ -715,45 +721,55 @@ __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* _
     xq.rest(x, k, 0, 1, lds, A, wave, lane);
     __syncthreads();
 
-    float acc[RR][1];
+    for (;;) {
+        float acc[RR][1];
 #pragma unroll
-    for (int r = 0; r < RR; r++) acc[r][0] = 0.0f;
-    for (uint32_t p = 0; p < npass; p++) {
-        if (p > 0) issue(p);
+        for (int r = 0; r < RR; r++) acc[r][0] = 0.0f;
+        for (uint32_t p = 0; p < npass; p++) {
+            if (p > 0) issue(p);
 #pragma unroll
-        for (int r = 0; r < RR; r++)
+            for (int r = 0; r < RR; r++)
 #pragma unroll
-            for (int v = 0; v < CPL; v++) {
-                const uint32_t c = lane + 64 * (v + CPL * p);
-                if (c < nchunks) compute_chunk<DT, 1>(ch[r][v], c, k, lds, A, acc[r]);
-            }
-    }
-    float out = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        float t = wave_sum(acc[r][0]);
-        if (GATE) {
-            const float u = wave_sum(acc[R + r][0]);
-            t = t / (1.0f + expf(0.0f - t)) * u;
-        }
-        if (lane == (uint32_t)r) out = t;
-    }
-    const uint32_t gr = row0 + lane;
-    if (lane < (uint32_t)R && gr < G.rows) {
-        if (GATE) {
-            G.y[0][gr] = out;
-        } else {
-            uint32_t t = 0, lr = gr;
-            if (G.count > 1 && gr >= G.row_end[0]) {
-                t = 1;
-                lr = gr - G.row_end[0];
-                if (G.count > 2 && gr >= G.row_end[1]) {
-                    t = 2;
-                    lr = gr - G.row_end[1];
+                for (int v = 0; v < CPL; v++) {
+                    const uint32_t c = lane + 64 * (v + CPL * p);
+                    if (c < nchunks) compute_chunk<DT, 1>(ch[r][v], c, k, lds, A, acc[r]);
                 }
-            }
-            G.y[t][lr] = out;
         }
+        // the next group's loads go out before this group's reduction
+        const uint32_t cur = row0, next = grp + gstride;
+        if (next < ngroups) {
+            grp = next;
+            row0 = next * R;
+            issue(0);
+        }
+        float out = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float t = wave_sum(acc[r][0]);
+            if (GATE) {
+                const float u = wave_sum(acc[R + r][0]);
+                t = t / (1.0f + expf(0.0f - t)) * u;
+            }
+            if (lane == (uint32_t)r) out = t;
+        }
+        const uint32_t gr = cur + lane;
+        if (lane < (uint32_t)R && gr < G.rows) {
+            if (GATE) {
+                G.y[0][gr] = out;
+            } else {
+                uint32_t t = 0, lr = gr;
+                if (G.count > 1 && gr >= G.row_end[0]) {
+                    t = 1;
+                    lr = gr - G.row_end[0];
+                    if (G.count > 2 && gr >= G.row_end[1]) {
+                        t = 2;
+                        lr = gr - G.row_end[1];
+                    }
+                }
+                G.y[t][lr] = out;
+            }
+        }
+        if (next >= ngroups) break;
     }
 }
 
@@ -811,8 +827,11 @@ hipError_t launch_group_one(const WGroup& g, const float* x, hipStream_t s) {
     const uint32_t lds = lds_bytes(1, g.w[0].k, kq);
     auto fn = group_kernel<DT, R, CPL, NW, GATE>;
     int ncu = 1;
-    (void)wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);  // sets the LDS limit once
-    const uint32_t grid = (g.rows + R * NW - 1) / (R * NW);
+    const int occ = wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);
+    const uint32_t need = (g.rows + R * NW - 1) / (R * NW);
+    static const bool one_shot = env_int("XNQ_GROUP_ONE_SHOT", 0) != 0;
+    const uint32_t cap = (uint32_t)(occ * ncu);
+    const uint32_t grid = one_shot || need < cap ? need : cap;
     hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, g, x);
     return hipGetLastError();
 }
