@@ -814,7 +814,13 @@ hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m
     const int occ = wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);
     const uint32_t ngroups = (w.n + R - 1) / R;
     const uint32_t need = (ngroups + NW - 1) / NW;
-    const uint32_t cap = (uint32_t)(occ * ncu);
+    // the fused Q4_K kernel runs one 16-wavefront workgroup per CU: each CU
+    // then quantizes the row once, not twice (4096 -> 14336 step 9.27 ->
+    // 8.82 us); Q4_0 (7.7 -> 9.4) and Q6_K (69.1 -> 69.7 on the lm_head)
+    // keep the full occupancy.  XNQ_MV_FUSED_OCC sets it (tuning).
+    static const int fused_occ = env_int("XNQ_MV_FUSED_OCC", 0);
+    const int wg_cu = !FUSED ? occ : fused_occ > 0 ? std::min(fused_occ, occ) : DT == XNQ_Q4K ? 1 : occ;
+    const uint32_t cap = (uint32_t)(wg_cu * ncu);
     const uint32_t grid = need < cap ? need : cap;
     hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, w, a, x, m0, mc, y);
     return hipGetLastError();
