@@ -67,6 +67,13 @@ def test_act_quantizer_edge_values(orc, dev):
         rng.normal(0, 1e6, k).astype(np.float32),
         rng.normal(0, 1e-6, k).astype(np.float32),
     ]
+    # a NaN (dropped from the block maximum; its quant is min(NaN, 127) = 127
+    # for Q8_K, `NaN as i8` = 0 for Q8_0) and infinities (Rust `as i8`
+    # saturation and NaN products)
+    for pos, val in ((5, np.nan), (9, np.inf), (40, -np.inf)):
+        r = rng.normal(0, 1, k).astype(np.float32)
+        r[pos] = val
+        rows.append(r)
     x = np.stack(rows)
     for act in (Q8_0, Q8K):
         want = orc.from_float(act, x)

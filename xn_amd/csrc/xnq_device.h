@@ -11,12 +11,11 @@ namespace xnq {
 
 // ---- scalar semantics of the reference (Rust) -----------------------------
 
-// f32 `as i8`: saturating, NaN -> 0.
+// f32 `as i8`: saturating, NaN -> 0, else truncated toward zero.  Branch
+// free: NaN replaced by 0, clamped to [-128, 127] with med3, then converted.
 __device__ __forceinline__ int8_t f_as_i8(float v) {
-    if (v != v) return 0;
-    if (v <= -128.0f) return -128;
-    if (v >= 127.0f) return 127;
-    return (int8_t)(int)v;
+    const float c = __builtin_amdgcn_fmed3f(v == v ? v : 0.0f, -128.0f, 127.0f);
+    return (int8_t)(int)c;
 }
 __device__ __forceinline__ uint8_t f_as_u8(float v) {
     if (v != v) return 0;

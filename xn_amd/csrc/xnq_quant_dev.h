@@ -21,17 +21,16 @@ __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v)));
 }
 
-// Largest value over the wavefront of a non-negative (or NaN) float: lanes
-// shifted in from outside a row read 0, and fmaxf drops NaN like the
-// reference's strict `amax < |x|` comparison does.
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-    v = fmaxf(v, dpp_f<0x111>(v));
-    v = fmaxf(v, dpp_f<0x112>(v));
-    v = fmaxf(v, dpp_f<0x114>(v));
-    v = fmaxf(v, dpp_f<0x118>(v));
-    v = fmaxf(v, dpp_f<0x142, 0xa>(v));
-    v = fmaxf(v, dpp_f<0x143, 0xc>(v));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+// Largest value over the wavefront (lanes shifted in from outside a row read
+// 0, the identity here).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0x111>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x112>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x114>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x118>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x142, 0xa>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x143, 0xc>((int)v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // One 256-element Q8_K block per wavefront, elements 4*lane .. 4*lane+3 in `v`.
@@ -48,10 +47,15 @@ __device__ __forceinline__ Q8KLane q8k_quant_wave(float4 v, int lane) {
     // Largest |x|; the reference keeps the first index on ties (strict
     // `amax < |x|`), so its signed value is taken from the lowest lane, and
     // the lowest element in that lane, holding an |x| equal to the maximum.
-    float lmax = 0.0f;
+    // as bit patterns: non-negative floats order like their bits, and a NaN
+    // (above the infinity pattern) is dropped as 0, as fmaxf drops it
+    uint32_t lmax = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; i++) lmax = fmaxf(lmax, fabsf(xs[i]));
-    const float amax = wave_max_nonneg(lmax);
+    for (int i = 0; i < 4; i++) {
+        const uint32_t a = __float_as_uint(xs[i]) & 0x7fffffffu;
+        lmax = max(lmax, a > 0x7f800000u ? 0u : a);
+    }
+    const float amax = __uint_as_float(wave_max_u32(lmax));
     int8_t q[4] = {0, 0, 0, 0};
     float d = 0.0f;
     if (amax != 0.0f) {
