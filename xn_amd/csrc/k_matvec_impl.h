@@ -590,9 +590,10 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     // whole first row group; the activation image is built while the weight
     // loads travel.
     StagePrefetch<MB, NW> pre;
-    // one round of the fused quantizer covers 4096 elements of a row per
-    // 4 * 4 / NW blocks per wavefront (further rounds in xq.rest)
-    XQuant<DT, MB, NW, (NW >= 16 ? 1 : NW >= 8 ? 2 : 4)> xq;
+    // one round of the fused quantizer covers the row length one pass of
+    // the weight loads covers (64 * CPL chunks): 64 * CPL * 32 / 256 blocks
+    // over NW wavefronts (further rounds, for longer rows, in xq.rest)
+    XQuant<DT, MB, NW, (CPL * 8 + NW - 1) / NW> xq;
     if (FUSED) xq.load(x, w.k, m0, mcount, xq.first(wave), lane);
     else pre.load(a, m0, mcount);
     issue(min(g, ngroups - 1), 0);
