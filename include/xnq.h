@@ -113,9 +113,9 @@ xnq_status xnq_qtensor_matmul_t(const xnq_qtensor* qt, size_t m, size_t k, size_
 
 /* matmul_t with caller-owned scratch (no allocation inside): workspace_dev
  * holds at least xnq_qtensor_matmul_t_workspace_size(qt, m) bytes, which is
- * 0 on the fused decode route (m == 1 on weights of up to 6144 x 4096
- * elements, the row quantized in LDS by the matvec kernel; workspace_dev may
- * then be NULL).  Same contract as xnq_qtensor_matmul_t
+ * 0 on the fused decode route (m == 1 with K <= 4096, or on weights of up
+ * to 6144 x 4096 elements: the row quantized in LDS by the matvec kernel;
+ * workspace_dev may then be NULL).  Same contract as xnq_qtensor_matmul_t
  * (QTensor::matmul_t, mod.rs:334-339; k_quants::matmul, k_quants.rs:1996-2011). */
 size_t xnq_qtensor_matmul_t_workspace_size(const xnq_qtensor* qt, size_t m);
 xnq_status xnq_qtensor_matmul_t_ws(const xnq_qtensor* qt, size_t m, size_t k, size_t n,
