@@ -23,8 +23,7 @@ constexpr int kWave = 64;
 template <bool CANONICAL>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x,
                                                             size_t nblocks, ActImg A,
-                                                            uint8_t* __restrict__ out,
-                                                            uint8_t* __restrict__ tile, TileImg T) {
+                                                            uint8_t* __restrict__ out) {
     const int lane = threadIdx.x & (kWave - 1);
     const size_t blk = (size_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
     if (blk >= nblocks) return;  // uniform over the wavefront
@@ -40,21 +39,54 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
         const size_t bpr = A.k / 256;
         const size_t row = blk / bpr, sb = blk % bpr;
         q8k_store(out + row * A.row_bytes, A, (uint32_t)sb, lane, r);
-        if (tile) {
-            // lane's elements 4*lane .. 4*lane+3 of super-block sb: chunk
-            // 8*sb + lane/8 = stage 4*sb + lane/16, ks = (lane/8)&1, half (lane/4)&1
-            const size_t rb = row >> 6, r64 = row & 63;
-            const size_t st = 4 * sb + (lane >> 4), piece = (lane >> 2) & 3;  // ks * 2 + h
-            *reinterpret_cast<uint32_t*>(tile + rb * 64 * A.k + st * 4096 + piece * 1024 + r64 * 16 +
-                                         4 * (lane & 3)) = r.packed;
-            const size_t rs = rb * bpr + sb;
-            if (lane == 0) reinterpret_cast<float*>(tile + T.d_off + rs * 256)[r64] = r.d;
-            if ((lane & 3) == 0) {
-                const int g = lane >> 2;  // bsum group 0..15
-                reinterpret_cast<int16_t*>(tile + T.s_off + (rs * 2 + (r64 >> 5)) * 1024 + (g >> 3) * 512 +
-                                           (r64 & 31) * 16)[g & 7] = (int16_t)r.bsum;
-            }
-        }
+    }
+}
+
+// Q8_K activations for the prefill kernel: the row image plus its row-tiled
+// copy.  One workgroup of R wavefronts per (64-row block, super-block, R-row
+// group); wavefront w quantizes row w of the group.  Every R x 16-byte run of
+// the tiled copy (whole cache lines for R >= 8) is assembled in LDS and stored
+// by one workgroup, so no cache line of the copy is written piecewise from
+// workgroups that sit on different XCDs (different L2s).  Rows past m (the
+// padding of the last 64-row block) are stored as zeros.
+template <int R>
+__global__ __launch_bounds__(64 * R) void quantize_q8k_tiled_kernel(const float* __restrict__ x, uint32_t m,
+                                                                     ActImg A, uint8_t* __restrict__ out,
+                                                                     uint8_t* __restrict__ tile, TileImg T) {
+    static_assert(R == 8 || R == 16, "8 or 16 rows per workgroup");
+    constexpr uint32_t kGroups = 64 / R, kPitch = R * 16 + 16;  // + 16 bytes against LDS bank conflicts
+    __shared__ __align__(16) uint8_t sq[16 * kPitch];  // [stage * 4 + piece][row][16]
+    __shared__ __align__(16) float sd[R];              // d by row
+    __shared__ __align__(16) int16_t ss[2][R][8];      // bsums [half][row][g & 7]
+    const int lane = threadIdx.x & (kWave - 1), rr = threadIdx.x / kWave;
+    const uint32_t bpr = A.k / 256;
+    const uint32_t grp = blockIdx.x % kGroups, rest = blockIdx.x / kGroups;
+    const uint32_t sb = rest % bpr, rb = rest / bpr;
+    const uint32_t row = rb * 64 + grp * R + rr;
+    const float4 v = row < m ? reinterpret_cast<const float4*>(x + (size_t)row * A.k + (size_t)sb * 256)[lane]
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    const Q8KLane r = q8k_quant_wave(v, lane);
+    if (row < m) q8k_store(out + (size_t)row * A.row_bytes, A, sb, lane, r);
+    // lane's 4 quants: stage lane / 16, piece (lane / 4) & 3, bytes 4 * (lane & 3)
+    *reinterpret_cast<uint32_t*>(sq + (lane >> 2) * kPitch + rr * 16 + 4 * (lane & 3)) = r.packed;
+    if (lane == 0) sd[rr] = r.d;
+    if ((lane & 3) == 0) ss[lane >> 5][rr][(lane >> 2) & 7] = (int16_t)r.bsum;
+    __syncthreads();
+    const uint32_t t = threadIdx.x;
+    const size_t rs = (size_t)rb * bpr + sb;
+    const uint32_t r64 = grp * R;  // first row of the group in its 64-row block
+    if (t < 16 * R) {
+        const uint32_t seg = t / R, i = t % R;
+        const uint4 val = *reinterpret_cast<const uint4*>(sq + seg * kPitch + i * 16);
+        *reinterpret_cast<uint4*>(tile + (size_t)rb * 64 * A.k + (size_t)(4 * sb + (seg >> 2)) * 4096 +
+                                  (seg & 3) * 1024 + (r64 + i) * 16) = val;
+    } else if (t < 16 * R + R / 4) {
+        const uint32_t i = t - 16 * R;
+        reinterpret_cast<uint4*>(tile + T.d_off + rs * 256 + r64 * 4)[i] = reinterpret_cast<const uint4*>(sd)[i];
+    } else if (t >= 16 * R + 64 && t < 18 * R + 64) {  // the bsums from a wavefront of their own
+        const uint32_t i = t - (16 * R + 64), half = i / R, j = i % R;
+        *reinterpret_cast<uint4*>(tile + T.s_off + (rs * 2 + (r64 >> 5)) * 1024 + half * 512 + ((r64 & 31) + j) * 16) =
+            *reinterpret_cast<const uint4*>(&ss[half][j][0]);
     }
 }
 
@@ -691,8 +723,11 @@ hipError_t launch_quantize_act(const ALayout& L, const float* x, void* ws, hipSt
     if (L.m == 0) return hipSuccess;
     if (L.act_dtype == XNQ_Q8K) {
         const size_t nblocks = L.m * (L.k / 256);
-        quantize_q8k_kernel<false><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(
-            x, nblocks, L.img, b, L.tiled ? b + L.tile_off : nullptr, L.tile);
+        if (L.tiled)
+            quantize_q8k_tiled_kernel<8><<<(unsigned)(L.tile.rbs * (L.k / 256) * 8), 512, 0, s>>>(
+                x, (uint32_t)L.m, L.img, b, b + L.tile_off, L.tile);
+        else
+            quantize_q8k_kernel<false><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, L.img, b);
     } else {
         const size_t nblocks = L.m * (L.k / 32);
         quantize_q80_kernel<false><<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, nblocks, L.img, b);
@@ -707,7 +742,7 @@ hipError_t launch_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, co
     const ActImg A = act_img((uint32_t)k, act_dtype == XNQ_Q8K);
     if (act_dtype == XNQ_Q8K) {
         const size_t nblocks = m * (k / 256);
-        quantize_q8k_kernel<true><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, A, b, nullptr, TileImg{});
+        quantize_q8k_kernel<true><<<(unsigned)((nblocks + 3) / 4), 256, 0, s>>>(x, nblocks, A, b);
     } else {
         const size_t nblocks = m * (k / 32);
         quantize_q80_kernel<true><<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, nblocks, A, b);
