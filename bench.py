@@ -10,6 +10,11 @@ HBM.  Weight copies are rotated
 from the 256 MB Infinity Cache.  Steps are captured in a HIP graph and the
 graph replay is timed with HIP events on the capture stream.
 
+Unless --no-cpu is given, the outputs of the last timed replays (the M=1 row,
+16 sampled rows of the M=512 product) are compared with the CPU oracle on the
+same inputs and weights (`check` in the JSON line); bench.py exits with status
+1 when they differ beyond the parity tolerance.
+
 Prints one JSON line (see `result` below).
 """
 from __future__ import annotations
@@ -111,6 +116,20 @@ def time_graph(g, stream, reps: int = 5) -> float:
         end.synchronize()
         times.append(start.elapsed_time(end))
     return float(np.median(times))
+
+
+# The parity tolerance of the f32 outputs (the same as the GPU tests'):
+# relative L2 over the whole output, and per row the largest absolute error
+# relative to the row's largest |value|.
+REL_L2, ROW_MAX_REL = 1e-3, 2e-3
+
+
+def close_stats(got: np.ndarray, want: np.ndarray) -> tuple:
+    got = got.reshape(want.shape).astype(np.float64)
+    want = want.astype(np.float64)
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    row = np.abs(got - want).max(axis=1) / np.maximum(np.abs(want).max(axis=1), 1e-30)
+    return float(rel), float(row.max())
 
 
 WEIGHT_BYTES = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}  # dtype: (block elems, block bytes)
@@ -411,6 +430,7 @@ def main():
         return
 
     # ---------------- weights: rotated copies, quantized on the device
+    timed_out = {}  # what the timed graphs computed last: (copy index, lhs, output)
     copies = []
     for _ in range(args.copies):
         w = torch.randn((N_DIM, K_DIM), generator=gen, device=dev, dtype=torch.float32) * 0.02
@@ -449,6 +469,9 @@ def main():
         ms_step = time_graph(g_step, stream) / args.steps
         ms_kern = time_graph(g_kern, stream) / args.steps
         ms_split = time_graph(g_split, stream) / args.steps
+        # the last replayed step's output (every variant computes the same y
+        # for step i), kept for the check against the CPU oracle
+        timed_out["matvec"] = ((args.steps - 1) % len(copies), x.cpu().numpy(), y.cpu().numpy())
         result["matvec_variants_us"] = {
             "matmul_t_step": round(ms_step * 1e3, 3),
             "preq_kernel": round(ms_kern * 1e3, 3),
@@ -503,6 +526,7 @@ def main():
             gk = capture(pkern, psteps, stream, args.eager)
         ms_p = time_graph(gp, stream) / psteps
         ms_k = time_graph(gk, stream) / psteps
+        timed_out["prefill"] = ((psteps - 1) % len(copies), xp.cpu().numpy(), yp.cpu().numpy())
         ops = 2.0 * m * N_DIM * K_DIM
         result["prefill"] = {
             "workload": f"q4k_qmatmul_m{m}_k{K_DIM}_n{N_DIM}",
@@ -518,11 +542,28 @@ def main():
             result["unit"] = "TOPS"
             result["ms_per_step"] = result["prefill"]["ms_per_call"]
 
+    # ---------------- check of the timed outputs against the CPU oracle
+    cpu_threads = min(os.cpu_count() or 1, 16)
+    if not args.no_cpu and timed_out:
+        import oracle
+
+        oracle.cpu_pool_init(cpu_threads)  # the first call fixes the pool size
+        check = {"rel_l2_max": REL_L2, "row_max_rel_max": ROW_MAX_REL}
+        ok = True
+        for name, (ci, lhs, got) in timed_out.items():
+            rows = np.arange(lhs.shape[0]) if lhs.shape[0] <= 16 else np.linspace(0, lhs.shape[0] - 1, 16).astype(int)
+            want = oracle.cpu_matmul(oracle.Q4K, lhs[rows], np.frombuffer(copies[ci].data(), dtype=np.uint8), N_DIM)
+            rel, row_rel = close_stats(got[rows], want)
+            ok = ok and rel <= REL_L2 and row_rel <= ROW_MAX_REL
+            check[name] = {"rows_checked": len(rows), "rel_l2": float(f"{rel:.3e}"), "row_max_rel": float(f"{row_rel:.3e}")}
+        check["ok"] = bool(ok)
+        result["check"] = check
+
     # ---------------- CPU baseline: the xn-style AVX2 path on the host cores
     if not args.no_cpu and args.only in ("all", "matvec"):
         import oracle
 
-        threads = min(os.cpu_count() or 1, 16)
+        threads = cpu_threads
         oracle.cpu_pool_init(threads)
         ncopies = min(16, len(copies))  # > 512 MB, past any host L3
         host_w = [np.frombuffer(copies[i].data(), dtype=np.uint8) for i in range(ncopies)]
@@ -560,6 +601,9 @@ def main():
         }
 
     print(json.dumps(result), flush=True)
+    if not result.get("check", {}).get("ok", True):
+        print("bench: the timed outputs differ from the CPU oracle beyond the tolerance", file=sys.stderr, flush=True)
+        sys.exit(1)
 
 
 if __name__ == "__main__":
