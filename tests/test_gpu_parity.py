@@ -170,10 +170,10 @@ def test_matmul_small(orc, dev, dt, m, entry):
     (Q4K, 4096, 1792),    # an 8-way column-parallel shard of gate/up
     (Q6K, 1792, 4096),    # an 8-way row-parallel shard of down
 ])
-# m = 4: the matvec, or for Q4_K / Q6_K weights of 2049-8192 rows the skinny
-# kernel; m = 5 and 8: the skinny kernel for Q4_K / Q6_K, the matvec for the
-# other dtypes
-@pytest.mark.parametrize("m", [1, 4, 5, 8])
+# m = 3 and 4: the matvec, or for Q4_K / Q6_K weights with K >= 4096 and
+# 2048 < N <= K the skinny kernel; m = 5 and 8: the skinny kernel for
+# Q4_K / Q6_K, the matvec for the other dtypes
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8])
 def test_matmul_config_shapes(orc, dev, dt, k, n, m):
     rng = np.random.default_rng(7000 + dt + k + n + m)
     w = rng.normal(0, 0.02, (n, k)).astype(np.float32)

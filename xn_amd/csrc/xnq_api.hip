@@ -457,18 +457,21 @@ static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced
     // below 32 rows.  At m = 5: 4096 x 4096 10.5 against 9.2, 4096 -> 14336
     // 13.9 against 13.9, 4096 -> 1792 8.7 / 8.5, Q6_K 1792 -> 4096 8.8 / 8.2,
     // Q6_K 4096 x 4096 11.7 / 10.2, 2048 x 2048 7.4 / 6.6; at m = 3 the
-    // matvec wins (7.3 / 8.4, 6.7 / 7.7, 8.7 / 10.2, 33.9 / 37.4 on
-    // 8192 -> 28672).  Groups: q/k/v at m = 2 13.4 against 10.6; the gate/up
-    // pair at m = 2 22.2 against 24.5, at m = 3 24.0 / 24.1.  At m = 4 the
-    // skinny kernel wins for single weights of about 4096 rows (4096 x 4096
-    // 8.6 against 7.5, 14336 -> 4096 17.0 / 13.1, Q6_K 14336 -> 4096
-    // 19.9 / 18.4) and loses for wide ones (4096 -> 14336 13.3 / 13.6,
-    // 8192 -> 28672 34.1 / 37.6).
-    const size_t skinny_lo = skinny_min                        ? skinny_min
-                             : group_n > 16384                 ? 3
-                             : group_n >= 6144                 ? 2
-                             : group_n == 0 && n > 2048 && n <= 8192 ? 4
-                                                               : 5;
+    // matvec wins for short or many rows (4096 -> 1792 7.2 / 7.3, Q6_K
+    // 1792 -> 4096 6.7 / 7.5, 8192 -> 28672 33.9 / 37.4).  Groups: q/k/v at m = 2 13.4 against 10.6; the gate/up
+    // pair at m = 2 22.2 against 24.5, at m = 3 24.0 / 24.1.  Single weights
+    // with K >= 4096 and 2048 < N <= K (few, long rows) take the skinny
+    // kernel from m = 3: 4096 x 4096 8.7 / 8.2 at m = 3 and 8.7 / 8.2 at
+    // m = 4, 14336 -> 4096 17.8 / 14.2 and 17.9 / 14.1, Q6_K 14336 -> 4096
+    // 19.4 / 18.0 and 19.8 / 18.0; the matvec keeps short or many rows
+    // (m = 4: Q6_K 1792 -> 4096 6.6 / 7.7, 4096 -> 6144 10.2 / 10.3,
+    // 4096 -> 14336 13.3 / 13.6, 4096 -> 1792 7.3 / 7.3).
+    const bool long_rows = group_n == 0 && k >= 4096 && n > 2048 && n <= k;
+    const size_t skinny_lo = skinny_min            ? skinny_min
+                             : group_n > 16384     ? 3
+                             : group_n >= 6144     ? 2
+                             : long_rows           ? 3
+                                                   : 5;
     if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
     if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
     return kMatvec;
