@@ -102,8 +102,9 @@ size_t xnq_qtensor_device_bytes(const xnq_qtensor* qt);
 /* dst[m x n] = lhs[m x k] . W^T, with lhs quantized to the weight's vec-dot
  * type first.  Replaces QTensor::matmul_t / QuantizedType::matmul_t /
  * k_quants::matmul (mod.rs:334-339, 221-223; k_quants.rs:1996-2011).  The
- * route is chosen from m: a wavefront-per-row matvec for small m (Q4_K /
- * Q6_K up to 4 rows), the small-batch int8 MFMA kernel up to 64 rows, the
+ * route is chosen from m and the shape: a wavefront-per-row matvec for small
+ * m (Q4_K / Q6_K up to 4 rows, up to 2 for K >= 4096 and 2048 < N <= K),
+ * the small-batch int8 MFMA kernel up to 64 rows, the
  * tiled int8 MFMA kernel for prefill-sized m.  Validates what xn validates:
  * mkn against the weight shape (repack.rs:203-215) and m*k == lhs length is
  * the caller's contract.  Stream ordered; allocates its activation scratch
