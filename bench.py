@@ -41,6 +41,19 @@ def weight_bytes(n: int, k: int) -> int:
     return n * (k // 256) * Q4K_BYTES_PER_SB
 
 
+GPU_BOX_CPU_SHARE = 16  # CPUs a one-GPU job may keep busy on the GPU boxes
+
+
+def host_threads() -> int:
+    """Threads of the CPU baseline pool: xn sizes its pool from
+    RAYON_NUM_THREADS, else num_cpus::get() (utils.rs:16-27); here the CPUs
+    this process may run on, capped at the GPU box's per-GPU CPU share."""
+    avail = len(os.sched_getaffinity(0))
+    env = os.environ.get("RAYON_NUM_THREADS", "")
+    want = int(env) if env.isdigit() and int(env) > 0 else avail
+    return max(1, min(want, avail, GPU_BOX_CPU_SHARE))
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -50,11 +63,10 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=512)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "stream", "probes", "sweep", "decode"],
+    p.add_argument("--only", choices=["all", "matvec", "prefill", "copy", "stream", "sweep", "decode"],
                    default="all",
                    help="'copy' times a plain 512 MiB device copy (calibrates the HBM byte counters); "
                         "'stream' times a bare read of the headline weight's bytes (the matvec's ceiling); "
-                        "'probes' measures the matrix-core / VALU issue sharing and the LDS read bandwidth; "
                         "'sweep' times every configured shape (matvec sweep, FFN, prefill, decode step)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one instead of replaying a HIP graph (for counter runs)")
@@ -312,50 +324,6 @@ def sweep(args, dev, stream, gen) -> dict:
     return {"metric": "per-config sweep", "rows": rows}
 
 
-CLOCK_GHZ = 2.4  # MI355X peak engine clock, used to turn times into cycles
-
-
-def probes(dev, stream) -> dict:
-    """Hardware ceilings behind the kernels' designs (measurement hooks in the
-    library): int8 MFMA with independent VALU work in the same wavefront
-    ("same") or in the other wavefront of each SIMD ("split"), and the LDS
-    read bandwidth.  One workgroup of 8 wavefronts per CU."""
-    import torch
-
-    from xn_amd.quantized import probe_lds_read, probe_mfma_valu
-
-    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
-    sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    iters = 4096
-
-    def timed(fn, reps=3):
-        with torch.cuda.stream(stream):
-            fn()
-            ts = []
-            for _ in range(reps):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                fn()
-                e1.record(stream)
-                e1.synchronize()
-                ts.append(e0.elapsed_time(e1))
-        return float(np.median(ts))
-
-    out = {"metric": "probes", "clock_ghz_assumed": CLOCK_GHZ, "mfma_valu": []}
-    for split in (False, True):
-        for rounds in (0, 2, 4, 8, 16):
-            ms = timed(lambda: probe_mfma_valu(rounds, split, iters, ncu, sink))
-            cyc = ms * 1e-3 * CLOCK_GHZ * 1e9 / iters
-            out["mfma_valu"].append({
-                "layout": "split" if split else "same", "valu_ops_per_wave_iter": 8 * rounds,
-                "mfma_per_simd_iter": 4 if split else 8, "cycles_per_iter": round(cyc, 1)})
-    ms = timed(lambda: probe_lds_read(iters, ncu, sink))
-    nbytes = ncu * 8 * 8 * 1024 * iters
-    out["lds_read"] = {"bytes_per_clk_per_cu": round(nbytes / ncu / (ms * 1e-3) / (CLOCK_GHZ * 1e9), 1),
-                       "chip_tb_s": round(nbytes / (ms * 1e-3) / 1e12, 1)}
-    return out
-
-
 def main():
     args = parse()
     if args.gpus != 1:
@@ -404,7 +372,7 @@ def main():
         return
 
     if args.only == "stream":
-        from xn_amd.quantized import stream_read
+        from xn_amd.measure import stream_read
 
         nbytes = weight_bytes(N_DIM, K_DIM)
         ncopy = max(2, (600 << 20) // nbytes + 1)  # past the 256 MB Infinity Cache
@@ -419,10 +387,6 @@ def main():
                           "bytes_per_launch": nbytes, "copies": ncopy, "us_per_read": round(ms * 1e3, 3),
                           "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                           "frac_of_8TBs": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
-        return
-
-    if args.only == "probes":
-        print(json.dumps(probes(dev, stream)), flush=True)
         return
 
     if args.only in ("sweep", "decode"):
@@ -543,7 +507,7 @@ def main():
             result["ms_per_step"] = result["prefill"]["ms_per_call"]
 
     # ---------------- check of the timed outputs against the CPU oracle
-    cpu_threads = min(os.cpu_count() or 1, 16)
+    cpu_threads = host_threads()
     if not args.no_cpu and timed_out:
         import oracle
 
@@ -593,6 +557,10 @@ def main():
             "value": round(algo_bytes / med / 1e9, 2),
             "unit": "GB/s",
             "cores": threads,
+            "host_cpus": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)),
+            "threads_rule": "xn's pool size (utils.rs:16-27: RAYON_NUM_THREADS, else every CPU the process may "
+                            f"use) capped at the GPU box's CPU share of {GPU_BOX_CPU_SHARE} per GPU",
             "kind": "port",
             "value_excl_quantize": round(algo_bytes / med_k / 1e9, 2),
             "sample": f"{len(times)} calls of Q4_K 4096->14336 M=1 (quantize_lhs + AVX2 vec_dot_q4k_q8k over "

@@ -236,29 +236,6 @@ xnq_status xnq_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const
 xnq_status xnq_qtensor_block_ints(const xnq_qtensor* qt, size_t m, const void* workspace_dev,
                                   int32_t* out_dev, void* stream);
 
-/* Measurement hook, no counterpart in the reference: reads `bytes` (a
- * multiple of 16) of device memory at `src_dev` with the matvec kernels'
- * access pattern (dwordx4, non-temporal, 4 loads in flight per lane, a grid
- * of 4-wavefront workgroups filling the GPU) and XORs every 32-bit word into
- * *sink_dev (which the caller zeroes).  Its time is the ceiling a weight
- * stream of that size reaches on this GPU. */
-xnq_status xnq_stream_read(const void* src_dev, size_t bytes, uint32_t* sink_dev, void* stream);
-
-/* Measurement hooks, no counterpart in the reference: the ceilings the
- * matmul kernels are measured against.
- *   xnq_probe_mfma_valu: workgroups of 8 wavefronts (2 per SIMD) loop
- *     `iters` times over 4 independent v_mfma_i32_32x32x32_i8 and
- *     8 * valu_rounds independent integer VALU ops (valu_rounds in
- *     0, 2, 4, 8, 16); split != 0 puts the MFMAs in wavefronts 0-3 and the
- *     VALU work in 4-7 (one of each per SIMD).  Timing it shows whether VALU
- *     time hides under the matrix cores.
- *   xnq_probe_lds_read: workgroups of 8 wavefronts each read 8 conflict-free
- *     ds_read_b128 per iteration (1 KiB per instruction).
- * Results only keep the work live; *sink_dev is not meaningful. */
-xnq_status xnq_probe_mfma_valu(int valu_rounds, int split, int iters, int workgroups, uint32_t* sink_dev,
-                               void* stream);
-xnq_status xnq_probe_lds_read(int iters, int workgroups, uint32_t* sink_dev, void* stream);
-
 /* Stream capture into a replayable graph (xn's Device::capture_begin /
  * capture_end / CaptureGraph::launch, cuda_backend/mod.rs:251-283): every
  * launch the library makes on `stream` between begin and end is recorded,

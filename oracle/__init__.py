@@ -68,7 +68,7 @@ def lib() -> ctypes.CDLL:
         L.orc_make_qkx1_quants_ex.restype = ctypes.c_float
         L.orc_make_qkx1_quants_ex.argtypes = [i, i, vp, i, vp, vp, vp]
         L.orc_make_qx_quants_ex.restype = ctypes.c_float
-        L.orc_make_qx_quants_ex.argtypes = [i, i, vp, vp, i, vp]
+        L.orc_make_qx_quants_ex.argtypes = [i, i, vp, vp, i, vp, vp]
         L.orc_make_q3_quants_ex.restype = ctypes.c_float
         L.orc_make_q3_quants_ex.argtypes = [vp, i, i, i, vp, vp]
         L.cpu_pool_init.restype = i
@@ -214,14 +214,18 @@ def make_qkx1_quants(nmax: int, ntry: int, x) -> tuple:
     return np.float32(s), nm[0], lv, int(info[0]), info[1], info[2]
 
 
-def make_qx_quants(nmax: int, x, rmse_type: int) -> tuple:
+def make_qx_quants(nmax: int, x, rmse_type: int, mid: bool = False) -> tuple:
     """utils.rs:65-202 -> (scale, levels (stored, 0..2*nmax-1), info:
-    [whole-block passes, per-element passes, changes in the last pass])."""
+    [whole-block passes, per-element passes, changes in the last pass,
+    whole-block passes kept]) and, with mid, the stored levels the
+    whole-block loop left."""
     x = _f32(x).reshape(-1)
     ls = np.zeros(x.size, np.int8)
-    info = np.zeros(3, np.int32)
-    s = lib().orc_make_qx_quants_ex(x.size, nmax, x.ctypes.data, ls.ctypes.data, rmse_type, info.ctypes.data)
-    return np.float32(s), ls, info
+    ls_mid = np.zeros(x.size, np.int8)
+    info = np.zeros(4, np.int32)
+    s = lib().orc_make_qx_quants_ex(x.size, nmax, x.ctypes.data, ls.ctypes.data, rmse_type, info.ctypes.data,
+                                    ls_mid.ctypes.data)
+    return (np.float32(s), ls, info, ls_mid) if mid else (np.float32(s), ls, info)
 
 
 def make_q3_quants(nmax: int, x, do_rmse: bool) -> tuple:

@@ -536,11 +536,13 @@ float orc_q4k_vec_dot(size_t n, const void* xv, const void* yv) {
 /* ------------------------------------------------------------ Q6_K */
 
 /* utils.rs:65-202 make_qx_quants.  The _ex form also reports, for the tests
- * that pin it, info[3] = {passes of the first (whole-block) refinement loop,
+ * that pin it, info[4] = {passes of the first (whole-block) refinement loop,
  * passes of the per-element loop, elements the last per-element pass
- * changed}; info may be NULL. */
-float orc_make_qx_quants_ex(int n, int nmax, const float* x, int8_t* ls, int rmse_type, int32_t* info) {
-    if (info) info[0] = info[1] = info[2] = 0;
+ * changed, whole-block passes whose levels were kept}, and the stored levels
+ * as the whole-block loop left them (ls_mid, n bytes); both may be NULL. */
+float orc_make_qx_quants_ex(int n, int nmax, const float* x, int8_t* ls, int rmse_type, int32_t* info,
+                            int8_t* ls_mid) {
+    if (info) info[0] = info[1] = info[2] = info[3] = 0;
     float max = 0.0f, amax = 0.0f;
     for (int i = 0; i < n; i++) {
         float ax = fabsf(x[i]);
@@ -594,7 +596,9 @@ float orc_make_qx_quants_ex(int n, int nmax, const float* x, int8_t* ls, int rms
         suml2 = sl2;
         scale = sumlx / suml2;
         best = scale * sumlx;
+        if (info) info[3] = itry + 1;
     }
+    if (ls_mid) memcpy(ls_mid, ls, (size_t)n);
     for (int itry = 0; itry < 5; itry++) {
         int n_changed = 0;
         if (info) info[1] = itry + 1;
@@ -649,7 +653,7 @@ float orc_make_qx_quants_ex(int n, int nmax, const float* x, int8_t* ls, int rms
 }
 
 float orc_make_qx_quants(int n, int nmax, const float* x, int8_t* ls, int rmse_type) {
-    return orc_make_qx_quants_ex(n, nmax, x, ls, rmse_type, NULL);
+    return orc_make_qx_quants_ex(n, nmax, x, ls, rmse_type, NULL, NULL);
 }
 
 /* k_quants.rs:1801-1871 BlockQ6K::from_float */

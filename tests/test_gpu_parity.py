@@ -461,7 +461,7 @@ def test_matmul_t_refuses_to_allocate_in_capture(orc, dev):
 def test_stream_read_folds_every_word(dev, nbytes):
     """The bare-read measurement hook reads every 32-bit word: its XOR fold
     equals numpy's, including a ragged tail past the last full round."""
-    from xn_amd.quantized import stream_read
+    from xn_amd.measure import stream_read
 
     host = np.random.default_rng(nbytes).integers(0, 2**32, nbytes // 4, dtype=np.uint32)
     buf = torch.from_numpy(host.view(np.uint8).copy()).to(dev)

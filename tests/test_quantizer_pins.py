@@ -187,6 +187,122 @@ def test_make_q3_quants_properties(orc):
     _symmetric_quantizer_case(lambda x: orc.make_q3_quants(4, x, True), 4, 300, 0, 1)
 
 
+def _wlsq_objective(x, l):
+    """sum(w x l)^2 / sum(w l^2) with w = x^2, in f64 (the quantity the
+    refinement loops of make_qx_quants / make_q3_quants maximise)."""
+    x = x.astype(np.float64)
+    l = l.astype(np.float64)
+    w = x * x
+    den = (w * l * l).sum()
+    return ((w * x * l).sum()) ** 2 / den if den > 0 else 0.0
+
+
+def _near_half(v):
+    """Elements whose nearest-integer rounding an f32 / f64 difference may flip."""
+    return np.abs(np.abs(v - np.trunc(v)) - 0.5) < EPS * np.maximum(1.0, np.abs(v))
+
+
+def test_make_qx_quants_whole_block_loop(orc):
+    """The first (whole-block) refinement loop of make_qx_quants
+    (utils.rs:113-139), from the levels it leaves and its pass counts:
+      * it starts from l0 = nearest(-nmax / max * x) (clamped) and runs at
+        most 3 passes; a pass whose levels are kept strictly raises the
+        objective, so kept passes end above l0 and differ from it;
+      * its first pass decides on the candidate nearest(x / scale0), scale0
+        the least-squares scale of l0: a candidate equal to l0 ends the loop
+        after one pass, a clearly better one (objective up by more than
+        1e-5 relative, well above f32 rounding) is kept;
+      * when it stopped before 3 kept passes, it stopped at the first pass
+        whose candidate levels nearest(x / scale) under the levels' own
+        least-squares scale either change nothing or do not raise the
+        objective (slx^2 <= best * sl2).
+    A flipped stop test or a dropped pass (clearly better candidates not
+    kept), an extra pass, or a candidate built from a stale scale breaks one
+    of these."""
+    nmax = 32
+    rng = np.random.default_rng(410)
+    blocks = _blocks(rng, 800, 16)
+    kept = np.zeros(4, int)
+    checked = clearly_better = 0
+    for x in blocks:
+        s, lv, info, mid = orc.make_qx_quants(nmax, x, 1, mid=True)
+        passes, kept_passes = int(info[0]), int(info[3])
+        if np.abs(x).max() == 0:
+            assert passes == 0
+            continue
+        assert 1 <= passes <= 3 and 0 <= kept_passes <= passes
+        assert kept_passes == 3 or passes == kept_passes + 1, info
+        kept[kept_passes] += 1
+        x64 = x.astype(np.float64)
+        amax_i = int(np.argmax(np.abs(x)))
+        t0 = -nmax / x64[amax_i] * x64
+        l0 = np.clip(_round_away(t0), -nmax, nmax - 1)
+        l = mid.astype(np.int64) - nmax
+        assert l.min() >= -nmax and l.max() <= nmax - 1
+        if _near_half(t0).any():
+            continue
+        f0, f = _wlsq_objective(x64, l0), _wlsq_objective(x64, l)
+        w = x64 * x64
+        t1 = x64 / ((w * x64 * l0).sum() / (w * l0 * l0).sum())
+        if not _near_half(t1).any():
+            cand1 = np.clip(_round_away(t1), -nmax, nmax - 1)
+            if np.array_equal(cand1, l0):
+                assert passes == 1 and kept_passes == 0, info
+            elif _wlsq_objective(x64, cand1) > f0 * (1 + 1e-5):
+                assert kept_passes >= 1, (x.tolist(), info)
+                clearly_better += 1
+        if kept_passes == 0:
+            assert np.array_equal(l, l0)
+        else:
+            assert not np.array_equal(l, l0) and f > f0 * (1 - EPS), (f, f0)
+        if kept_passes < 3:
+            w = x64 * x64
+            scale = (w * x64 * l).sum() / (w * l * l).sum()
+            t = x64 / scale
+            if _near_half(t).any():
+                continue
+            cand = np.clip(_round_away(t), -nmax, nmax - 1)
+            assert np.array_equal(cand, l) or _wlsq_objective(x64, cand) <= f * (1 + EPS), \
+                (x.tolist(), l.tolist(), cand.tolist())
+        checked += 1
+    # the distribution is not degenerate: blocks stop after 0, 1 and 2 kept passes
+    assert checked > 0.8 * len(blocks)
+    assert kept[0] > 0 and kept[1] > 0 and clearly_better > 20, (kept, clearly_better)
+
+
+def test_make_q3_quants_initial_levels(orc):
+    """make_q3_quants' counterpart of the whole-block start (utils.rs:275-284):
+    its per-element loop starts from l0 = round(-nmax / max * x) clamped to
+    -nmax..nmax-1 (max the signed element of largest magnitude).  When that
+    loop's first pass changes nothing, the returned levels are exactly l0 and
+    the returned scale is their weighted least-squares scale; the
+    non-rmse path returns l0 and 1 / iscale."""
+    nmax = 4
+    rng = np.random.default_rng(420)
+    blocks = _blocks(rng, 800, 16)
+    untouched = 0
+    for x in blocks:
+        if np.abs(x).max() == 0:
+            continue
+        x64 = x.astype(np.float64)
+        amax_i = int(np.argmax(np.abs(x)))
+        t0 = -nmax / x64[amax_i] * x64
+        if _near_half(t0).any():
+            continue
+        l0 = np.clip(_round_away(t0), -nmax, nmax - 1)
+        s, lv, info = orc.make_q3_quants(nmax, x, False)
+        assert np.array_equal(lv.astype(np.int64) - nmax, l0)
+        assert abs(s - x64[amax_i] / -nmax) <= 1e-6 * abs(s)
+        s, lv, info = orc.make_q3_quants(nmax, x, True)
+        if info[0] == 1 and info[1] == 0:
+            untouched += 1
+            assert np.array_equal(lv.astype(np.int64) - nmax, l0)
+            w = x64 * x64
+            want = (w * x64 * l0).sum() / (w * l0 * l0).sum()
+            assert abs(s - want) <= 1e-4 * abs(want)
+    assert untouched > 10
+
+
 # ------------------------------------------------------------ from_float, block level
 def _f16(v):
     return np.float32(np.float16(np.float32(v)))

@@ -61,9 +61,6 @@ SIGNATURES = {
     "xnq_qtensor_raw_data": (c_int, [c_void, c_void, c_size, c_void]),
     "xnq_quantize_act_blocks": (c_int, [c_u32, c_size, c_size, c_void, c_void, c_void]),
     "xnq_qtensor_block_ints": (c_int, [c_void, c_size, c_void, c_void, c_void]),
-    "xnq_stream_read": (c_int, [c_void, c_size, c_void, c_void]),
-    "xnq_probe_mfma_valu": (c_int, [c_int, c_int, c_int, c_int, c_void, c_void]),
-    "xnq_probe_lds_read": (c_int, [c_int, c_int, c_void, c_void]),
 }
 
 STATUS = {0: "XNQ_OK", 1: "XNQ_ERR_INVALID", 2: "XNQ_ERR_UNSUPPORTED", 3: "XNQ_ERR_HIP", 4: "XNQ_ERR_OOM"}

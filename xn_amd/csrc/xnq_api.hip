@@ -93,9 +93,13 @@ xnq_status check_weight(uint32_t dtype, size_t n, size_t k) {
         return fail(XNQ_ERR_INVALID,
                     "quantized tensor must have their last dim divisible by block size [%zu, %zu] %zu",
                     n, k, bs);
-    // kernels address every plane with 32-bit byte offsets (Q4K / Q6K planes
-    // pad the rows to a multiple of 128)
-    if (n > 0xffffffffull || k > 0x7fffffffull || (n + 127) / 128 * 128 * (k / bs) * type_size(dtype) >= (1ull << 32))
+    // kernels address every plane with 32-bit byte offsets; the largest plane
+    // holds at most type_size bytes per block (raw layouts: the padded
+    // stride), over the rows (Q4K / Q6K: padded to a multiple of 128 for
+    // their tiled header copies)
+    const size_t rows = (dtype == XNQ_Q4K || dtype == XNQ_Q6K) ? (n + 127) / 128 * 128 : n;
+    const size_t per_block = is_raw_layout(dtype) ? raw_stride(dtype) : type_size(dtype);
+    if (n > 0xffffffffull || k > 0x7fffffffull || rows * (k / bs) * per_block >= (1ull << 32))
         return fail(XNQ_ERR_INVALID, "tensor too large for the device layout [%zu, %zu]", n, k);
     return XNQ_OK;
 }
@@ -803,9 +807,11 @@ size_t xnq_matmul_t_silu_gate_workspace_size(const xnq_qtensor* gate, const xnq_
     return silu_gate_ws_impl(gate, up, m, g_route.load());
 }
 
-xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
-                                  const float* lhs_dev, void* workspace_dev, size_t workspace_bytes, float* dst_dev,
-                                  void* stream) {
+// `forced` is the route override as read once at the public entry point
+// (xnq_matmul_t_silu_gate or xnq_mlp_t), so sizing and launching agree.
+static xnq_status silu_gate_impl(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
+                                 const float* lhs_dev, void* workspace_dev, size_t workspace_bytes, float* dst_dev,
+                                 void* stream, int forced) {
     xnq_status st = check_mkn(gate, m, k, n);
     if (st) return st;
     st = check_mkn(up, m, k, n);
@@ -813,7 +819,6 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     if (gate->device != up->device) return fail(XNQ_ERR_INVALID, "gate and up live on different devices");
     if (m == 0 || n == 0) return XNQ_OK;
     if (!lhs_dev || !dst_dev) return fail(XNQ_ERR_INVALID, "null pointer");
-    const int forced = g_route.load();
     const size_t need = silu_gate_ws_impl(gate, up, m, forced);
     hipStream_t s = (hipStream_t)stream;
     if (need == 0) {
@@ -855,6 +860,12 @@ xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up
     const hipError_t e = launch_silu_mul(dst_dev, u, m * n, s);
     if (e != hipSuccess) return hip_fail(e, "silu_mul kernel");
     return XNQ_OK;
+}
+
+xnq_status xnq_matmul_t_silu_gate(const xnq_qtensor* gate, const xnq_qtensor* up, size_t m, size_t k, size_t n,
+                                  const float* lhs_dev, void* workspace_dev, size_t workspace_bytes, float* dst_dev,
+                                  void* stream) {
+    return silu_gate_impl(gate, up, m, k, n, lhs_dev, workspace_dev, workspace_bytes, dst_dev, stream, g_route.load());
 }
 
 // ---------------------------------------------------------------------------
@@ -913,7 +924,7 @@ xnq_status xnq_mlp_t(const xnq_qtensor* gate, const xnq_qtensor* up, const xnq_q
         if (!st) st = matmul_preq_impl(down, m, f, down->L.n, wsb, bytes_b, dst_dev, stream, forced);
         return st;
     }
-    st = xnq_matmul_t_silu_gate(gate, up, m, k, f, lhs_dev, workspace_dev, a, h_dev, stream);
+    st = silu_gate_impl(gate, up, m, k, f, lhs_dev, workspace_dev, a, h_dev, stream, forced);
     if (!st) st = matmul_t_ws_impl(down, m, f, down->L.n, h_dev, wsb, bytes_b, dst_dev, stream, forced);
     return st;
 }
@@ -1054,30 +1065,6 @@ struct xnq_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
-
-xnq_status xnq_stream_read(const void* src_dev, size_t bytes, uint32_t* sink_dev, void* stream) {
-    if (bytes % 16) return fail(XNQ_ERR_INVALID, "stream_read: %zu bytes is not a multiple of 16", bytes);
-    if (bytes && (!src_dev || !sink_dev)) return fail(XNQ_ERR_INVALID, "null pointer");
-    const hipError_t e = launch_stream_read(src_dev, bytes, sink_dev, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "stream_read kernel");
-    return XNQ_OK;
-}
-
-xnq_status xnq_probe_mfma_valu(int valu_rounds, int split, int iters, int workgroups, uint32_t* sink_dev,
-                               void* stream) {
-    if (iters < 1 || workgroups < 1 || !sink_dev) return fail(XNQ_ERR_INVALID, "probe: bad arguments");
-    const hipError_t e = launch_probe_mfma_valu(valu_rounds, split != 0, iters, workgroups, sink_dev, (hipStream_t)stream);
-    if (e == hipErrorInvalidValue) return fail(XNQ_ERR_INVALID, "probe: valu_rounds must be 0, 2, 4, 8 or 16");
-    if (e != hipSuccess) return hip_fail(e, "probe kernel");
-    return XNQ_OK;
-}
-
-xnq_status xnq_probe_lds_read(int iters, int workgroups, uint32_t* sink_dev, void* stream) {
-    if (iters < 1 || workgroups < 1 || !sink_dev) return fail(XNQ_ERR_INVALID, "probe: bad arguments");
-    const hipError_t e = launch_probe_lds_read(iters, workgroups, sink_dev, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "probe kernel");
-    return XNQ_OK;
-}
 
 xnq_status xnq_capture_begin(void* stream) {
     if (!stream) return fail(XNQ_ERR_INVALID, "stream capture needs a stream other than the null stream");

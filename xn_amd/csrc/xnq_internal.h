@@ -221,11 +221,6 @@ hipError_t set_max_lds(const void* kernel, int bytes);
 hipError_t launch_repack(const WLayout& L, const void* gguf_dev, void* dst_dev, hipStream_t s);
 hipError_t launch_unrepack(const WLayout& L, const void* src_dev, void* gguf_dev, hipStream_t s);
 hipError_t launch_dequant(const WLayout& L, const void* src_dev, float* y, hipStream_t s);
-// k_probe.hip (measurement hooks)
-hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s);
-hipError_t launch_probe_mfma_valu(int valu_rounds, bool split, int iters, int workgroups, uint32_t* sink,
-                                  hipStream_t s);
-hipError_t launch_probe_lds_read(int iters, int workgroups, uint32_t* sink, hipStream_t s);
 // k_quantize.hip
 hipError_t launch_quantize_act(const ALayout& A, const float* x, void* ws, hipStream_t s);
 hipError_t launch_quantize_act_blocks(uint32_t act_dtype, size_t m, size_t k, const float* x,

@@ -506,25 +506,6 @@ class capture:
 
 # -- lower-level entry points used by tests and the benchmark ------------------
 
-def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
-    """Bare read of `buf`'s bytes folded by XOR into the int32 `sink`
-    (xnq_stream_read): the weight-stream ceiling, for measurement."""
-    if not buf.is_cuda or not buf.is_contiguous() or sink.dtype != torch.int32 or not sink.is_cuda:
-        raise XnqError(1, "stream_read: contiguous device buffer and an int32 device sink")
-    check(_lib.load().xnq_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream(buf.device)))
-
-
-def probe_mfma_valu(valu_rounds: int, split: bool, iters: int, workgroups: int, sink: torch.Tensor) -> None:
-    """Measurement hook xnq_probe_mfma_valu (int8 MFMA chains with independent VALU work)."""
-    check(_lib.load().xnq_probe_mfma_valu(int(valu_rounds), int(bool(split)), int(iters), int(workgroups), _ptr(sink),
-                                          _stream(sink.device)))
-
-
-def probe_lds_read(iters: int, workgroups: int, sink: torch.Tensor) -> None:
-    """Measurement hook xnq_probe_lds_read (conflict-free ds_read_b128 stream)."""
-    check(_lib.load().xnq_probe_lds_read(int(iters), int(workgroups), _ptr(sink), _stream(sink.device)))
-
-
 def set_route(route: int) -> None:
     """0 = route by m, 1 = force the matvec kernel, 2 = force the MFMA kernel."""
     check(_lib.load().xnq_set_route(int(route)))
