@@ -666,6 +666,7 @@ hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits
     // the kernel reads the row-tiled activation image, which must cover m rows
     if (!a.tile || (size_t)a.T.rbs * 64 < m || a.k != w.k) return hipErrorInvalidValue;
     if (splits > 1 && !partial) splits = 1;
+    if (prefill_supported(w.dtype, m, w.n, w.k)) return launch_prefill(w, a, m, splits, y, partial, s);
     if (w.dtype == XNQ_Q4K) return launch_dt<XNQ_Q4K>(w, a, m, splits, y, partial, s);
     if (w.dtype == XNQ_Q6K) return launch_dt<XNQ_Q6K>(w, a, m, splits, y, partial, s);
     return hipErrorNotSupported;

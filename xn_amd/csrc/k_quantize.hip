@@ -87,6 +87,13 @@ __global__ __launch_bounds__(64 * R) void quantize_q8k_tiled_kernel(const float*
         const uint32_t i = t - (16 * R + 64), half = i / R, j = i % R;
         *reinterpret_cast<uint4*>(tile + T.s_off + (rs * 2 + (r64 >> 5)) * 1024 + half * 512 + ((r64 & 31) + j) * 16) =
             *reinterpret_cast<const uint4*>(&ss[half][j][0]);
+    } else if (t >= 18 * R + 64 && t < 20 * R + 64) {  // the Q4K min-term operand
+        const uint32_t i = t - (18 * R + 64), half = i / R, j = i % R;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = -sd[j] * (float)((int)ss[half][j][2 * u] + (int)ss[half][j][2 * u + 1]);
+        *reinterpret_cast<uint4*>(tile + T.x_off + (rs * 2 + (r64 >> 5)) * 1024 + half * 512 + ((r64 & 31) + j) * 16) =
+            bf16_hilo4(v);
     }
 }
 

@@ -486,8 +486,8 @@ static size_t partial_offset(uint32_t dtype, size_t m, size_t k, int forced) {
     return (act_layout(dtype, m, k, forced).bytes + kAlign - 1) / kAlign * kAlign;
 }
 
-static uint32_t route_splits(Route r, size_t m, size_t n, size_t k) {
-    if (r == kMfma) return mfma_splits(m, n, k);
+static uint32_t route_splits(Route r, uint32_t dtype, size_t m, size_t n, size_t k) {
+    if (r == kMfma) return prefill_supported(dtype, m, n, k) ? prefill_splits(m, n, k) : mfma_splits(m, n, k);
     if (r == kSkinny) return skinny_splits(m, n, k);
     return 1;
 }
@@ -496,7 +496,7 @@ static size_t workspace_size_impl(const xnq_qtensor* qt, size_t m, int forced) {
     if (!qt) return 0;
     const size_t k = qt->L.k, n = qt->L.n;
     size_t bytes = act_layout(qt->L.dtype, m, k, forced).bytes;
-    const uint32_t splits = route_splits(pick_route(qt->L.dtype, m, n, k, forced), m, n, k);
+    const uint32_t splits = route_splits(pick_route(qt->L.dtype, m, n, k, forced), qt->L.dtype, m, n, k);
     if (splits > 1) bytes = partial_offset(qt->L.dtype, m, k, forced) + (size_t)splits * m * n * sizeof(float);
     return bytes;
 }
@@ -520,7 +520,7 @@ static xnq_status matmul_preq_impl(const xnq_qtensor* qt, size_t m, size_t k, si
     if (r == kMfma || r == kSkinny) {
         if (r == kMfma ? !mfma_supported(qt->L.dtype, m, n, k) : !skinny_supported(qt->L.dtype, m, n, k))
             return fail(XNQ_ERR_UNSUPPORTED, "no MFMA kernel for this dtype/shape");
-        uint32_t splits = route_splits(r, m, n, k);
+        uint32_t splits = route_splits(r, qt->L.dtype, m, n, k);
         const size_t off = partial_offset(qt->L.dtype, m, k, forced);
         if (off + (size_t)splits * m * n * sizeof(float) > workspace_bytes) splits = 1;
         float* partial = splits > 1 ? reinterpret_cast<float*>((uint8_t*)workspace_dev + off) : nullptr;

@@ -49,6 +49,22 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
     return (float)h;
 }
 
+// Four f32 values as bf16 high parts (round to nearest even) and bf16
+// remainders (v - hi, so hi + lo carries ~16 significant bits), packed as
+// 16 bytes: the 4 high parts, then the 4 remainders.
+__device__ __forceinline__ uint4 bf16_hilo4(const float* v) {
+    typedef __bf16 v4bf_t __attribute__((ext_vector_type(4)));
+    v4bf_t h, l;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const __bf16 hb = (__bf16)v[t];
+        h[t] = hb;
+        l[t] = (__bf16)(v[t] - (float)hb);
+    }
+    const uint2 hu = __builtin_bit_cast(uint2, h), lu = __builtin_bit_cast(uint2, l);
+    return make_uint4(hu.x, hu.y, lu.x, lu.y);
+}
+
 // ---- packed integer dots ---------------------------------------------------
 
 __device__ __forceinline__ int dot4(int a, int b, int c) {

@@ -128,9 +128,12 @@ __host__ __device__ inline uint32_t act_q_off(uint32_t k, uint32_t e) {
 //   quants  [rb][stage = 64 K][ks][h][row 64][16]: chunk 2*stage+ks, bytes 16h..16h+15
 //   d       [rb][sb][row 64] f32
 //   bsums   [rb][sb][row / 32][half][row % 32][16]: int16 bsums 8*half..8*half+7
+//   xmin    [rb][sb][row / 32][half][row % 32][16]: the Q4K min-term operand of
+//           sub-blocks 4*half..4*half+3, v_j = -d * (bsum[2j] + bsum[2j+1]),
+//           as 4 bf16 high parts then 4 bf16 remainders (v - hi)
 struct TileImg {
     uint32_t rbs = 0;  // 64-row blocks
-    size_t d_off = 0, s_off = 0, bytes = 0;
+    size_t d_off = 0, s_off = 0, x_off = 0, bytes = 0;
 };
 
 __host__ __device__ inline TileImg tile_img(size_t m, uint32_t k) {
@@ -139,7 +142,8 @@ __host__ __device__ inline TileImg tile_img(size_t m, uint32_t k) {
     const size_t nsb = k / 256;
     T.d_off = (size_t)T.rbs * 64 * k;
     T.s_off = T.d_off + (size_t)T.rbs * nsb * 256;
-    T.bytes = T.s_off + (size_t)T.rbs * nsb * 2048;
+    T.x_off = T.s_off + (size_t)T.rbs * nsb * 2048;
+    T.bytes = T.x_off + (size_t)T.rbs * nsb * 2048;
     return T;
 }
 
@@ -273,5 +277,10 @@ hipError_t launch_sum_silu_quant(const SumGroup& S, uint32_t splits, size_t m, s
                                  void* img, hipStream_t s);
 hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                        hipStream_t s);
+// k_prefill.hip: the Q4K matrix-core kernel with in-register weight expansion
+bool prefill_supported(uint32_t dtype, size_t m, size_t n, size_t k);
+uint32_t prefill_splits(size_t m, size_t n, size_t k);
+hipError_t launch_prefill(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
+                          hipStream_t s);
 
 }  // namespace xnq
