@@ -14,12 +14,13 @@
 // dmin*m_j (built per super-block from the block header, same split), on the
 // bf16 matrix cores into the f32 output (two K = 16 products).
 //
-// Tiling: a workgroup of 8 wavefronts (two per SIMD) owns a 128 x 256 output
-// tile; wavefront w owns columns 32w..32w+31 and all 128 rows: 4 tiles of
-// v_mfma_i32_32x32x32_i8 (hi and lo int32 sums plus the f32 output: 192
-// accumulator registers).  Each wavefront expands only its own columns'
-// weights, in registers, right before the MFMAs that use them, so no digit
-// plane goes through LDS; the activation tile is shared through LDS.
+// Tiling: a workgroup of 8 wavefronts (two per SIMD) owns 32*TM activation
+// rows (TM = 2 or 4 row tiles) by 256 weight columns; wavefront w owns
+// columns 32w..32w+31 and all TM row tiles of v_mfma_i32_32x32x32_i8 (hi and
+// lo int32 sums plus the f32 output: 192 accumulator registers at TM = 4).
+// Each wavefront expands only its own columns' weights, in registers, right
+// before the MFMAs that use them, so no digit plane goes through LDS; the
+// activation tile is shared through LDS.
 //
 // One MFMA K-step is 32 K: lane (column c, half g) contributes the low
 // (ks = 0) or high (ks = 1) nibbles of chunk 2p + g of the stage's chunk pair
@@ -29,19 +30,19 @@
 // already inside the digits.
 //
 // Data movement: every byte a stage needs is fetched with global_load_lds
-// DMA straight into LDS, three stages ahead: the activation tile (one 1 KiB
-// piece per wavefront and stage) into a shared 6-slot ring; per super-block
-// the min-term operand rows and d_a (shared, 4 buffers); per wavefront its
-// own weight chunks (1 KiB per stage, 4-slot ring) and block headers (one
-// 1 KiB fetch per super-block, 2 buffers).  One s_barrier per stage
-// publishes the shared pieces; each wavefront waits only for its own DMA
-// (s_waitcnt vmcnt with the exact count of younger DMA it issued).
+// DMA straight into LDS, three time steps ahead: the activation tile into a
+// shared 4-slot ring; per super-block the min-term operand rows and d_a
+// (shared, 4 buffers); per wavefront its own weight chunks (2 KiB per stage,
+// 3-slot ring) and block headers (one 1 KiB fetch per super-block, 2
+// buffers).  One s_barrier per time step publishes the shared pieces; each
+// wavefront waits only for its own DMA (s_waitcnt vmcnt with the exact count
+// of younger DMA it issued).
 //
-// Lead and lag: wavefronts 4-7 (the second wavefront of every SIMD) run two
-// stages behind wavefronts 0-3 over the same activation ring, so the two
-// wavefronts of a SIMD reach their super-block epilogues (about 4 VALU
-// instructions per MFMA) at different stages and each one's epilogue VALU
-// issues under the other's MFMAs.
+// Lead and lag: wavefronts 4-7 (the second wavefront of every SIMD) run the
+// same sequence of steps one time step behind wavefronts 0-3 over the same
+// activation ring, so the two wavefronts of a SIMD reach their super-block
+// epilogues (about 4 VALU instructions per MFMA) at different time steps and
+// each one's epilogue VALU issues under the other's MFMAs.
 #include <type_traits>
 
 #include "xnq_device.h"
