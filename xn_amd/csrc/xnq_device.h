@@ -105,20 +105,21 @@ __device__ __forceinline__ int nib_dot(uint4 q, const int* a) {
 
 // Q4K: 6-bit scale and min of sub-block j from the 12 packed bytes
 // (utils.rs:53-63 get_scale_min_k4); s0,s1,s2 = scales bytes 0-3, 4-7, 8-11.
-__device__ __forceinline__ uint32_t byte_of3(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
-    uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-    return (w >> (8 * (i & 3))) & 0xffu;
-}
+// Branch-free: both cases are "a nibble of one byte | the top 2 bits of
+// another << 4" on byte jj = j & 3 of one of the three dwords:
+//   j < 4:  sc = q[j] & 63          = nib(s0, 0) | top2(s0, 4)
+//           m  = q[j + 4] & 63      = nib(s1, 0) | top2(s1, 4)
+//   j >= 4: sc = (q[j + 4] & 15) | (q[j - 4] >> 6) << 4 = nib(s2, 0) | top2(s0, 6)
+//           m  = (q[j + 4] >> 4) | (q[j] >> 6) << 4     = nib(s2, 4) | top2(s1, 6)
+// so a lane-dependent j costs two selects and four bit-field extracts, not
+// both sides of a divergent branch.
 __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
                                               int& sc, int& m) {
-    if (j < 4) {
-        sc = (int)(byte_of3(s0, s1, s2, j) & 63u);
-        m = (int)(byte_of3(s0, s1, s2, j + 4) & 63u);
-    } else {
-        uint32_t bj4 = byte_of3(s0, s1, s2, j + 4);
-        sc = (int)((bj4 & 0xFu) | ((byte_of3(s0, s1, s2, j - 4) >> 6) << 4));
-        m = (int)((bj4 >> 4) | ((byte_of3(s0, s1, s2, j) >> 6) << 4));
-    }
+    const bool hi = j >= 4;
+    const uint32_t b = 8u * (uint32_t)(j & 3), o = hi ? 6u : 4u;
+    const uint32_t xs = hi ? s2 : s0, xm = hi ? s2 : s1, om = hi ? 4u : 0u;
+    sc = (int)(__builtin_amdgcn_ubfe(xs, b, 4) | (__builtin_amdgcn_ubfe(s0, b + o, 2) << 4));
+    m = (int)(__builtin_amdgcn_ubfe(xm, b + om, 4) | (__builtin_amdgcn_ubfe(s1, b + o, 2) << 4));
 }
 
 // All eight 6-bit scales and mins of a Q4K block header at once, four per
