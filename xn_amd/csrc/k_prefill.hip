@@ -30,10 +30,10 @@
 // already inside the digits.
 //
 // Data movement: every byte a stage needs is fetched with global_load_lds
-// DMA straight into LDS, three time steps ahead: the activation tile into a
+// DMA straight into LDS, two time steps ahead: the activation tile into a
 // shared 4-slot ring; per super-block the min-term operand rows and d_a
 // (shared, 4 buffers); per wavefront its own weight chunks (2 KiB per stage,
-// 3-slot ring) and block headers (one 1 KiB fetch per super-block, 2
+// 3-slot ring) and block headers (one 1 KiB fetch per super-block, 3
 // buffers).  One s_barrier per time step publishes the shared pieces; each
 // wavefront waits only for its own DMA (s_waitcnt vmcnt with the exact count
 // of younger DMA it issued).
@@ -41,8 +41,9 @@
 // Lead and lag: wavefronts 4-7 (the second wavefront of every SIMD) run the
 // same sequence of steps one time step behind wavefronts 0-3 over the same
 // activation ring, so the two wavefronts of a SIMD reach their super-block
-// epilogues (about 4 VALU instructions per MFMA) at different time steps and
-// each one's epilogue VALU issues under the other's MFMAs.
+// epilogues (about 4 VALU instructions per output element) at different time
+// steps and each one's epilogue VALU issues beside the other's MFMAs.
+#include <cstdlib>
 #include <type_traits>
 
 #include "xnq_device.h"
@@ -61,27 +62,28 @@ typedef unsigned short pf_v2u16 __attribute__((ext_vector_type(2)));
 constexpr int kPBN = 256, kPWaves = 8, kPThreads = kPWaves * 64;
 
 // Time line.  A stage is 128 K (two chunk pairs, four MFMA K-steps, 32 MFMAs
-// per wavefront).  Per super-block every wavefront runs three steps: stage
-// 2sb, stage 2sb+1 and an epilogue step E(sb) (the super-block's epilogue,
-// then the next super-block's header, digit scales and min-term products).
-// Wavefronts 0-3 ("lead") run step u of that sequence at time u, wavefronts
-// 4-7 ("lag") at time u + 1, so at every time one wavefront of each SIMD is
-// in an MFMA stage while the other may be in its VALU-heavy epilogue step:
-//   time 3sb:   lead stage 2sb     lag E(sb-1)
-//   time 3sb+1: lead stage 2sb+1   lag stage 2sb
-//   time 3sb+2: lead E(sb)         lag stage 2sb+1
-// Every DMA is issued three time steps before its first use.
+// per wavefront).  Per super-block every wavefront runs two steps:
+//   A(sb): epilogue of sb - 1, setup of sb (its header's digit scales, d_w,
+//          the min-term products), stage 2sb
+//   B(sb): stage 2sb + 1
+// so own step q runs stage q.  Wavefronts 0-3 ("lead") run own step q at
+// time q, wavefronts 4-7 ("lag") at time q + 1: at every time step both
+// wavefronts of a SIMD have a stage of MFMAs and one of them also the
+// super-block's VALU work.  (A time line of three steps per super-block,
+// with the epilogue in a step of its own, left one wavefront per SIMD
+// without MFMAs in two steps of three: 2-5 % slower at 128-384 rows.)
 
 // LDS map (bytes) for TM 32-row tiles per wavefront (BM = 32 TM rows)
 template <int TM>
 struct PLay {
+    static constexpr int kHdrBufs = 3;  // header buffers (super-block % 3)
     static constexpr int kBM = 32 * TM;
     static constexpr int kASlots = 4, kASlot = TM / 2 * 8192;  // [rb][half stage][ks2][h2][row 64][16]
     static constexpr int kRawSlots = 3, kRawSlot = kPWaves * 2048;  // [wave][pair][lane][16]
     static constexpr int kOffA = 0;
     static constexpr int kOffRaw = kOffA + kASlots * kASlot;
-    static constexpr int kOffHdr = kOffRaw + kRawSlots * kRawSlot;  // [sb & 1][wave][lane][16]
-    static constexpr int kOffX = kOffHdr + 2 * kPWaves * 1024;       // [sb & 3][row / 32][half][row % 32][16]
+    static constexpr int kOffHdr = kOffRaw + kRawSlots * kRawSlot;  // [sb % kHdrBufs][wave][lane][16]
+    static constexpr int kOffX = kOffHdr + kHdrBufs * kPWaves * 1024;  // [sb & 3][row / 32][half][row % 32][16]
     static constexpr int kOffDa = kOffX + 4 * TM * 1024;             // [sb & 3][row] f32
     static constexpr int kOffDw = kOffDa + 4 * 512;  // [wave][column] f32 d_w of the current super-block
     static constexpr int kLds = kOffDw + kPWaves * 128;
@@ -118,24 +120,13 @@ __device__ __forceinline__ uint32_t mulb(uint32_t d, uint32_t s2) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_v2u16, d) * __builtin_bit_cast(pf_v2u16, s2));
 }
 
-// DMA instructions a wavefront of group G issues at a time step of phase F
-// (time % 3): the activation pieces of the stage the lead runs three steps
-// later (2, none when that is an epilogue step), at F = 2 the min-term / d_a
-// piece of super-block sb + 2; its own weight chunks of its stage three
-// steps ahead (2, at its stage steps) or the headers of super-block sb + 2
-// (1, at its epilogue step).
-template <int G, int TM>
-constexpr int dma_count(int F) {
-    const int own = (F - G + 3) % 3;
-    return (F < 2 ? TM / 2 : 1) + (own < 2 ? 2 : 1);
-}
-
 template <int TM>
 __global__ __launch_bounds__(kPThreads) void prefill_q4k_kernel(WView w, AView a, uint32_t m, uint32_t m_tiles,
                                                                 uint32_t n_tiles, uint32_t splits,
                                                                 uint32_t sb_per_split, float* __restrict__ y,
                                                                 size_t split_stride) {
     using Lay = PLay<TM>;
+    constexpr int kHdrBufs = Lay::kHdrBufs;
     constexpr int kPTM = TM, kPBM = Lay::kBM, kASlots = Lay::kASlots, kASlot = Lay::kASlot;
     constexpr int kRawSlots = Lay::kRawSlots, kRawSlot = Lay::kRawSlot;
     constexpr int kOffA = Lay::kOffA, kOffRaw = Lay::kOffRaw, kOffHdr = Lay::kOffHdr, kOffX = Lay::kOffX;
@@ -203,7 +194,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_q4k_kernel(WView w, AView a
     };
     auto issue_hdr = [&](uint32_t sb) {
         const uint32_t sbc = min(sb, nsb - 1);
-        pdma16(w.st + (size_t)(sb0 + sbc) * 2048, hdr_off, lbase + kOffHdr + (sb & 1) * 8192 + wave * 1024);
+        pdma16(w.st + (size_t)(sb0 + sbc) * 2048, hdr_off, lbase + kOffHdr + (sb % kHdrBufs) * 8192 + wave * 1024);
     };
 
     pf_v16f accf[kPTM];
@@ -218,7 +209,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_q4k_kernel(WView w, AView a
     const uint32_t M4 = 0x0F0F0F0Fu;
 
     // Both groups run the same code over their own step index q (lead: time
-    // q, lag: time q + 1); the group only selects, uniformly per wavefront,
+    // q, lag: time q + 1); the group only decides, uniformly per wavefront,
     // which shared DMA a step issues and how many of its DMA may still be in
     // flight at the step's barrier.
     const uint32_t G = wave >> 2;
@@ -229,13 +220,15 @@ __global__ __launch_bounds__(kPThreads) void prefill_q4k_kernel(WView w, AView a
     // Setup of super-block sb from its headers: digit scales, d_w for the
     // epilogue, and the min-term products into the output.
     auto setup = [&](uint32_t sb) {
-        const uint4 hd = *reinterpret_cast<const uint4*>(lds + kOffHdr + (sb & 1) * 8192 + wave * 1024 + lane * 16);
+        const uint4 hd =
+            *reinterpret_cast<const uint4*>(lds + kOffHdr + (sb % kHdrBufs) * 8192 + wave * 1024 + lane * 16);
         const Q4KScales qs = q4k_scales(hd.y, hd.z, hd.w);
         sh_lo = (qs.sc_lo >> 3) & 0x07070707u;
         sl_lo = qs.sc_lo & 0x07070707u;
         sh_hi = (qs.sc_hi >> 3) & 0x07070707u;
         sl_hi = qs.sc_hi & 0x07070707u;
-        if (g == 0) reinterpret_cast<float*>(lds + kOffDw + wave * 128)[lrow] = f16_bits_to_f32(hd.x & 0xffffu);
+        // both lane halves hold column lrow's header: the same value, no branch
+        reinterpret_cast<float*>(lds + kOffDw + wave * 128)[lrow] = f16_bits_to_f32(hd.x & 0xffffu);
         // min term: column operand dmin * m_j for j = 4g .. 4g+3
         const float dm = f16_bits_to_f32(hd.x >> 16);
         const uint32_t mv = g ? qs.m_hi : qs.m_lo;
@@ -319,68 +312,67 @@ __global__ __launch_bounds__(kPThreads) void prefill_q4k_kernel(WView w, AView a
         }
     };
 
-    // Own step q of own phase PS = q mod 3 (compile-time): stage 2 (q/3) + PS
-    // for PS < 2, else E(q/3).  The time is t = q + G; WL / WG are the wait
-    // counts of the lead / lag at this step.
-    auto step = [&](int q, auto psc, auto wlc, auto wgc) {
-        constexpr int PS = decltype(psc)::value;
-        if (G) wait_and_barrier<decltype(wgc)::value>();
-        else wait_and_barrier<decltype(wlc)::value>();
-        // shared: the lead's step t + 3, of the time phase (PS + G) % 3
-        const uint32_t t = (uint32_t)(q + (int)G);
-        const uint32_t F = (PS + G) % 3, sbl = (t + 3) / 3;
-        if (F < 2) issue_stage(2 * sbl + F);
-        else issue_sb_shared(sbl + 1);  // used from E(sbl) on (min term of sbl + 1)
-        // own: the step three ahead (same own phase)
-        const uint32_t sbo = (uint32_t)(q + 3) / 3;  // own super-block of step q + 3
-        if (PS < 2) issue_own(2 * sbo + PS);
-        else issue_hdr(sbo + 1);  // read at E(sbo)
-        const int sbq = (q + 3) / 3 - 1;  // floor(q / 3) for q >= -1
-        if (PS < 2) {
-            if (q >= 0 && (uint32_t)sbq < nsb) stage(2 * (uint32_t)sbq + PS, std::integral_constant<int, PS>{});
-        } else {
-            if (q >= 0 && (uint32_t)sbq < nsb) epilogue((uint32_t)sbq);
-            if ((uint32_t)(sbq + 1) < nsb) setup((uint32_t)(sbq + 1));
+    {
+        // DMA is issued two time steps ahead: at time t the activation pieces
+        // of stage t + 2 and, at even t, the min-term / d_a pieces of
+        // super-block t / 2 + 1; at own step q the wavefront's weight chunks
+        // of stage q + 2 and, at even q, the headers of super-block q / 2 + 1.
+        // KIND (compile-time, so each step's work is one basic block the
+        // scheduler can interleave): 0 setup(0) + stage 0; 1 epilogue(sb - 1)
+        // + setup(sb) + stage 2 sb; 2 the last epilogue; 3 stage q (odd);
+        // 4 no work (the lag's time 0, the lead's last time step).
+        auto step2 = [&](int q, auto kindc, auto wlc, auto wgc) {
+            constexpr int KIND = decltype(kindc)::value;
+            constexpr int PS = (KIND == 3 || KIND == 4) ? 1 : 0;
+            if (G) wait_and_barrier<decltype(wgc)::value>();
+            else wait_and_barrier<decltype(wlc)::value>();
+            const uint32_t t = (uint32_t)(q + (int)G);
+            issue_stage(t + 2);
+            if ((t & 1u) == 0) issue_sb_shared(t / 2 + 1);
+            issue_own((uint32_t)(q + 2));
+            if (PS == 0) issue_hdr((uint32_t)(q / 2 + 1));
+            const uint32_t sb = (uint32_t)q / 2;
+            if constexpr (KIND == 0) {
+                setup(0);
+                stage(0, std::integral_constant<int, 0>{});
+            } else if constexpr (KIND == 1) {
+                epilogue(sb - 1);
+                setup(sb);
+                stage((uint32_t)q, std::integral_constant<int, 0>{});
+            } else if constexpr (KIND == 2) {
+                epilogue(sb - 1);
+            } else if constexpr (KIND == 3) {
+                stage((uint32_t)q, std::integral_constant<int, 1>{});
+            }
+        };
+        issue_stage(0);
+        issue_stage(1);
+        issue_sb_shared(0);
+        issue_own(0);
+        issue_own(1);
+        issue_hdr(0);
+        wait_and_barrier<0>();
+        using K0 = std::integral_constant<int, 0>;
+        using K1 = std::integral_constant<int, 1>;
+        using K2 = std::integral_constant<int, 2>;
+        using K3 = std::integral_constant<int, 3>;
+        using K4 = std::integral_constant<int, 4>;
+        using WZ = std::integral_constant<int, 0>;
+        // wait counts: the DMA this wavefront issued at the previous time step
+        using WL0 = std::integral_constant<int, TM / 2 + 2>;  // lead, even step (previous: odd time)
+        using WL1 = std::integral_constant<int, TM / 2 + 4>;  // lead, odd step
+        using WG = std::integral_constant<int, TM / 2 + 3>;   // lag, every step
+        if (G) step2(-1, K4{}, WZ{}, WZ{});  // the lag's time 0
+        step2(0, K0{}, WZ{}, WG{});
+        step2(1, K3{}, WL1{}, WG{});
+        for (uint32_t sb = 1; sb < nsb; sb++) {
+            step2((int)(2 * sb), K1{}, WL0{}, WG{});
+            step2((int)(2 * sb + 1), K3{}, WL1{}, WG{});
         }
-    };
-
-    // prologue: stages 0 and 1 (shared, own), super-blocks 0 and 1's
-    // min-term / d_a pieces and headers
-    issue_stage(0);
-    issue_stage(1);
-    issue_sb_shared(0);
-    issue_sb_shared(1);
-    issue_own(0);
-    issue_own(1);
-    issue_hdr(0);
-    issue_hdr(1);
-    wait_and_barrier<0>();
-
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    // wait counts: at time t everything issued up to time t - 3 must have
-    // landed, so the DMA of times t - 1 and t - 2 may be in flight
-    constexpr int L0 = dma_count<0, TM>(0), L1 = dma_count<0, TM>(1), L2 = dma_count<0, TM>(2);
-    constexpr int G0 = dma_count<1, TM>(0), G1 = dma_count<1, TM>(1), G2 = dma_count<1, TM>(2);
-    using WZ = std::integral_constant<int, 0>;
-    // the lag's own step -1 (time 0): only the setup of super-block 0; the
-    // lead sets super-block 0 up before its first step
-    if (G) step(-1, S2{}, WZ{}, WZ{});
-    else setup(0);
-    // first period: times 0 / 1 wait for the prologue / all but one step's DMA
-    step(0, S0{}, WZ{}, std::integral_constant<int, G0>{});
-    step(1, S1{}, std::integral_constant<int, L0>{}, std::integral_constant<int, G0 + G1>{});
-    step(2, S2{}, std::integral_constant<int, L0 + L1>{}, std::integral_constant<int, G1 + G2>{});
-    int q = 3;
-    for (uint32_t sb = 1; sb < nsb; sb++, q += 3) {
-        step(q, S0{}, std::integral_constant<int, L1 + L2>{}, std::integral_constant<int, G2 + G0>{});
-        step(q + 1, S1{}, std::integral_constant<int, L2 + L0>{}, std::integral_constant<int, G0 + G1>{});
-        step(q + 2, S2{}, std::integral_constant<int, L0 + L1>{}, std::integral_constant<int, G1 + G2>{});
+        step2((int)(2 * nsb), K2{}, WL0{}, WG{});  // the last epilogue
+        if (!G) step2((int)(2 * nsb + 1), K4{}, WL1{}, WZ{});  // the lead's last time step
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    // the lead's last time step (the lag ran its extra step first)
-    if (!G) step(q, S0{}, std::integral_constant<int, L1 + L2>{}, WZ{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // ---- write the tile: lane (lrow, g) of tile i holds row m0 + 32i + lrow,
     //      columns 8q + 4g .. 8q + 4g + 3 of the wavefront's 32 ----
@@ -421,9 +413,15 @@ static int prefill_tm(size_t m, size_t n) {
 // 512 71.9 / 74.0, 1024 145.1 / 151.2).
 constexpr size_t kPrefillMaxRows = 384;
 
+static int env_int_pf(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+
 bool prefill_supported(uint32_t dtype, size_t m, size_t n, size_t k) {
     (void)n;
-    return dtype == XNQ_Q4K && k % 256 == 0 && k >= 256 && m <= kPrefillMaxRows;
+    static const size_t max_rows = (size_t)env_int_pf("XNQ_PREFILL_MAX_ROWS", (int)kPrefillMaxRows);
+    return dtype == XNQ_Q4K && k % 256 == 0 && k >= 256 && m <= max_rows;
 }
 
 uint32_t prefill_splits(size_t m, size_t n, size_t k) {
