@@ -172,12 +172,12 @@ def test_config4_prefill(checker, weights, dev, dt):
     assert_close(y.cpu().numpy(), checker.cpu_matmul(dt, x, blocks, n), f"config 4 dt={dt} preq m=512")
 
 
-@pytest.mark.parametrize("m", [96, 384, 385])
+@pytest.mark.parametrize("m", [96, 384, 512, 513])
 def test_config4_prefill_route_boundary(checker, weights, dev, m):
     """Config 4's Q4_K weight on either side of the row count where the
     prefill route switches kernels: 64-row tiles with the K range split
-    across workgroups (m = 96), 128-row tiles (m = 384) and, past it, the
-    256 x 128 tiled kernel (m = 385)."""
+    across workgroups (m = 96), 128-row tiles (m = 384, 512) and, past it,
+    the 256 x 128 tiled kernel (m = 513)."""
     k, n = 4096, 14336
     qt, blocks = weights.get(Q4K, n, k)
     x = x_rows(m, k, SEED + 31 * m)

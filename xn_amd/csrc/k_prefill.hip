@@ -274,40 +274,54 @@ __global__ __launch_bounds__(kPThreads) void prefill_q4k_kernel(WView w, AView a
         }
     };
 
-    // Stage st = 2 sb + P2 (P2 compile-time): chunk pairs 2 P2 and 2 P2 + 1.
+    // Stage st = 2 sb + P2 (P2 compile-time): chunk pairs 2 P2 and 2 P2 + 1,
+    // four K-steps of TM fragment pairs.  The activation fragment of the
+    // (K-step, tile) kAhead positions later is read before each MFMA pair,
+    // and the second raw chunk two K-steps before its use, so the MFMAs issue
+    // back to back instead of each pair waiting on its own LDS read (the
+    // scheduler, left alone, sinks every read next to its use).
     auto stage = [&](uint32_t st, auto pc) {
         constexpr int P2 = decltype(pc)::value;
+        constexpr int kN = 4 * kPTM, kAhead = 4;
         const uint8_t* raw = lds + kOffRaw + (st % kRawSlots) * kRawSlot + wave * 2048 + lane * 16;
         const uint8_t* abase = lds + kOffA + (st % kASlots) * kASlot + g * 2048 + lrow * 16;
         const uint32_t shw = P2 == 0 ? sh_lo : sh_hi, slw = P2 == 0 ? sl_lo : sl_hi;
+        auto frag = [&](int j) {  // fragment j = kk * TM + i
+            const int kk = j / kPTM, i = j % kPTM, pp = kk >> 1, ks = kk & 1;
+            return *reinterpret_cast<const pf_v4i*>(abase + (i >> 1) * 8192 + pp * 4096 + ks * 1024 + (i & 1) * 512);
+        };
+        pf_v4i av[kN];
 #pragma unroll
-        for (int pp = 0; pp < 2; pp++) {
-            // this lane's chunk 2p + g (p = 2 P2 + pp) and its sub-block's digits
-            const uint4 rq = *reinterpret_cast<const uint4*>(raw + pp * 1024);
-            const uint32_t sel = pp ? sel1 : sel0;
-            const uint32_t sh2 = __builtin_amdgcn_perm(shw, shw, sel), sl2 = __builtin_amdgcn_perm(slw, slw, sel);
+        for (int j = 0; j < kAhead; j++) av[j] = frag(j);
+        uint4 rq = *reinterpret_cast<const uint4*>(raw);
+        const uint4 rqn = *reinterpret_cast<const uint4*>(raw + 1024);
+        pf_v4i bh, bl;
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
+        for (int j = 0; j < kN; j++) {
+            const int kk = j / kPTM, i = j % kPTM;
+            if (i == 0) {
+                // this lane's chunk 2p + g (p = 2 P2 + pp) and its sub-block's digits
+                const int pp = kk >> 1, ks = kk & 1;
+                if (kk == 2) rq = rqn;
+                const uint32_t sel = pp ? sel1 : sel0;
+                const uint32_t sh2 = __builtin_amdgcn_perm(shw, shw, sel), sl2 = __builtin_amdgcn_perm(slw, slw, sel);
                 uint32_t d[4];
                 if (ks == 0) {
                     d[0] = rq.x & M4; d[1] = rq.y & M4; d[2] = rq.z & M4; d[3] = rq.w & M4;
                 } else {
                     d[0] = (rq.x >> 4) & M4; d[1] = (rq.y >> 4) & M4; d[2] = (rq.z >> 4) & M4; d[3] = (rq.w >> 4) & M4;
                 }
-                const pf_v4i bh = {(int)mulb(d[0], sh2), (int)mulb(d[1], sh2), (int)mulb(d[2], sh2), (int)mulb(d[3], sh2)};
-                const pf_v4i bl = {(int)mulb(d[0], sl2), (int)mulb(d[1], sl2), (int)mulb(d[2], sl2), (int)mulb(d[3], sl2)};
-#pragma unroll
-                for (int i = 0; i < kPTM; i++) {
-                    const pf_v4i av =
-                        *reinterpret_cast<const pf_v4i*>(abase + (i >> 1) * 8192 + pp * 4096 + ks * 1024 + (i & 1) * 512);
-                    if (P2 == 0 && pp == 0 && ks == 0) {
-                        hi[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bh, av, pf_v16i{}, 0, 0, 0);
-                        lo[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bl, av, pf_v16i{}, 0, 0, 0);
-                    } else {
-                        hi[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bh, av, hi[i], 0, 0, 0);
-                        lo[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bl, av, lo[i], 0, 0, 0);
-                    }
-                }
+                bh = pf_v4i{(int)mulb(d[0], sh2), (int)mulb(d[1], sh2), (int)mulb(d[2], sh2), (int)mulb(d[3], sh2)};
+                bl = pf_v4i{(int)mulb(d[0], sl2), (int)mulb(d[1], sl2), (int)mulb(d[2], sl2), (int)mulb(d[3], sl2)};
+            }
+            if (j + kAhead < kN) av[j + kAhead] = frag(j + kAhead);
+            __builtin_amdgcn_sched_barrier(0);
+            if (P2 == 0 && kk == 0) {
+                hi[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bh, av[j], pf_v16i{}, 0, 0, 0);
+                lo[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bl, av[j], pf_v16i{}, 0, 0, 0);
+            } else {
+                hi[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bh, av[j], hi[i], 0, 0, 0);
+                lo[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bl, av[j], lo[i], 0, 0, 0);
             }
         }
     };
@@ -407,11 +421,12 @@ static int prefill_tm(size_t m, size_t n) {
 }
 
 // Where this kernel replaces the tiled kernel of k_mfma.hip: Q4_K up to
-// 384 rows (K = 4096 -> N = 14336, HIP graph steps, µs, tiled against this
-// kernel: m = 96 46.7 / 33.5, 128 50.6 / 35.3, 192 66.3 / 48.0, 256
-// 64.5 / 49.8, 384 72.0 / 68.7; from m = 512 on the tiled kernel is ahead:
-// 512 71.9 / 74.0, 1024 145.1 / 151.2).
-constexpr size_t kPrefillMaxRows = 384;
+// 512 rows.  K = 4096 -> N = 14336, HIP graph steps, µs, tiled kernel
+// against this one, on one box: m = 128 50.6 / 33.6, 256 64.5 / 48.5, 384
+// 72.0 / 70.9, 512 81.9 / 74.1, 1024 155.0 / 147.6; on others 512 ran
+// 82.2 / 76.1 and 83.2 / 83.2, 768 136.2 / 138.8.  Past 512 the tiled
+// kernel stays (XNQ_PREFILL_MAX_ROWS moves the limit, tuning).
+constexpr size_t kPrefillMaxRows = 512;
 
 static int env_int_pf(const char* name, int dflt) {
     const char* v = std::getenv(name);
