@@ -244,6 +244,20 @@ size_t skinny_max_rows() {
     return v;
 }
 
+// Single Q4_K weights take the prefill kernel (k_prefill.hip, 64-row tiles)
+// above this many rows: 4096 -> 14336, graph steps, µs, skinny against
+// prefill: m = 32 17.4 / 19.9, 40 24.0 / 20.9, 48 24.6 / 21.7, 56 24.4 /
+// 22.0, 64 25.8 / 23.2.  q/k/v groups and gate/up pairs keep the skinny
+// kernel's one launch over all their weights.
+static size_t skinny_q4k_max_rows() {
+    static const size_t v = env_size("XNQ_SKINNY_Q4K_MAX_ROWS", 32);
+    return v;
+}
+static bool q4k_prefill_early(uint32_t dtype, size_t m, size_t k) {
+    return dtype == XNQ_Q4K && m > skinny_q4k_max_rows() && m <= skinny_max_rows() &&
+           prefill_supported(dtype, m, 0, k);
+}
+
 // Whether the prefill (tiled MFMA) route can be taken for m activation rows,
 // in which case the activation quantizer also writes the row-tiled image.
 // It depends on m and the forced route, not on n, so xnq_quantize_lhs (which
@@ -253,7 +267,8 @@ size_t skinny_max_rows() {
 // xnq_set_route must not change.
 static bool tiled_act(uint32_t weight_dtype, size_t m, size_t k, int forced) {
     if (forced == 1 || forced == 3) return false;
-    return mfma_supported(weight_dtype, m, 0, k) && (forced == 2 || m > skinny_max_rows());
+    return mfma_supported(weight_dtype, m, 0, k) &&
+           (forced == 2 || m > skinny_max_rows() || q4k_prefill_early(weight_dtype, m, k));
 }
 
 ALayout act_layout(uint32_t weight_dtype, size_t m, size_t k, int forced) {
@@ -476,6 +491,7 @@ static Route pick_route(uint32_t dtype, size_t m, size_t n, size_t k, int forced
                              : group_n >= 6144     ? 2
                              : long_rows           ? 3
                                                    : 5;
+    if (group_n == 0 && q4k_prefill_early(dtype, m, k) && mfma_supported(dtype, m, n, k)) return kMfma;
     if (m >= skinny_lo && m <= skinny_max && skinny_supported(dtype, m, n, k)) return kSkinny;
     if (m > skinny_max && mfma_supported(dtype, m, n, k)) return kMfma;
     return kMatvec;
