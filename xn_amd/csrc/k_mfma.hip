@@ -12,7 +12,7 @@
 // work: w = sc_j * q does not fit int8, so it is split into two int8 digit
 // planes and contracted twice,
 //   Q4K: sc = 8*sh + sl (sh, sl in 0..7):  w = 8*(sh*q) + (sl*q), digits <= 105
-//   Q6K: w = sc*(q-32) in -4096..4096:      w = 128*(w >> 7) + (w & 127)
+//   Q6K: w = sc*(q-32) in -3968..4096:      w = 256*hi + lo, hi = (w+128) >> 8, lo signed
 // giving the exact integer I1 (resp. I) per super-block; the f32 epilogue then
 // applies d_a * d_w once per super-block.  The Q4K min term is a GEMM over
 // the 8 sub-blocks of a super-block with f32 operands -d_a*bsum32 and
@@ -254,19 +254,21 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale.
+// Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale:
+// w = sc * (q - 32) in [-3968, 4096]; w + 128 = 256 * hi + u with u in
+// [0, 255], so w = 256 * hi + lo with hi = byte 1 of w + 128 (in [-15, 16])
+// and lo = u - 128 (byte 0 of w + 128 with its top bit flipped).
 __device__ __forceinline__ void q6_digits(uint32_t q, int sc, uint32_t& lo, uint32_t& hi) {
-    const v2s x01 = {(short)(q & 0xFF), (short)((q >> 8) & 0xFF)};
-    const v2s x23 = {(short)((q >> 16) & 0xFF), (short)(q >> 24)};
-    // (q - 32) * sc as q * sc + (-32 sc): one packed multiply-add per pair
+    // bytes 0, 1 and 2, 3 of q zero-extended to 16-bit lanes
+    const v2s x01 = __builtin_bit_cast(v2s, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+    const v2s x23 = __builtin_bit_cast(v2s, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+    // (q - 32) * sc + 128 as q * sc + (128 - 32 sc): one packed multiply-add per pair
     const v2s s2 = {(short)sc, (short)sc};
-    const v2s c2 = {(short)(-32 * sc), (short)(-32 * sc)};
-    const v2s w01 = x01 * s2 + c2, w23 = x23 * s2 + c2;
-    const v2s m7 = {127, 127};
-    const v2s l01 = w01 & m7, l23 = w23 & m7;
-    const v2s h01 = w01 >> 7, h23 = w23 >> 7;
-    lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, l23), __builtin_bit_cast(uint32_t, l01), 0x06040200u);
-    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
+    const v2s c2 = {(short)(128 - 32 * sc), (short)(128 - 32 * sc)};
+    const uint32_t w01 = __builtin_bit_cast(uint32_t, x01 * s2 + c2);
+    const uint32_t w23 = __builtin_bit_cast(uint32_t, x23 * s2 + c2);
+    lo = __builtin_amdgcn_perm(w23, w01, 0x06040200u) ^ 0x80808080u;
+    hi = __builtin_amdgcn_perm(w23, w01, 0x07050301u);
 }
 
 // 4 floats -> bf16 hi | bf16 lo (v = hi + lo to ~16 significant bits), packed as 16 bytes
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         for (int j = 0; j < kTN; j++) accf[i][j] = v16f{};
 
     // ---- super-block epilogue of tile (i, j): y += d_a d_w (hi * 2^s + lo) [- d_a dmin I2] ----
-    constexpr int kShift = kQ4K ? 3 : 7;
+    constexpr int kShift = kQ4K ? 3 : 8;
     auto epilogue_tile = [&](uint32_t sb, int i, int j) {
         const uint8_t* epi = epi_base(sb);
         const float* eda = reinterpret_cast<const float*>(epi + L::kEDa);

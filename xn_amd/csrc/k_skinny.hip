@@ -16,7 +16,7 @@
 // above that one or two 32-row tiles on v_mfma_i32_32x32x32_i8.  Per
 // super-block each wavefront expands its columns' chunks from LDS into the
 // two int8 digit planes of the prefill kernel (Q4K: sc = 8*sh + sl, digits
-// sh*q and sl*q; Q6K: sc*(q-32) = 128*hi + lo), contracts them with the
+// sh*q and sl*q; Q6K: sc*(q-32) = 256*hi + lo), contracts them with the
 // activation tile and applies d_a * d_w in an f32 epilogue; the Q4K min term
 // is a GEMM of -d_a*bsum32 by dmin*m_j on the bf16 matrix cores.  The integer sums per super-block are exact, as in the reference's
 // block dots (k_quants.rs:1337-1416, 1743-1798).  When the column tiles alone
@@ -160,19 +160,21 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, d) * s2);
 }
 
-// Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale.
+// Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale:
+// w = sc * (q - 32) in [-3968, 4096]; w + 128 = 256 * hi + u with u in
+// [0, 255], so w = 256 * hi + lo with hi = byte 1 of w + 128 (in [-15, 16])
+// and lo = u - 128 (byte 0 of w + 128 with its top bit flipped).
 __device__ __forceinline__ void q6_digits(uint32_t q, int sc, uint32_t& lo, uint32_t& hi) {
-    const v2s x01 = {(short)(q & 0xFF), (short)((q >> 8) & 0xFF)};
-    const v2s x23 = {(short)((q >> 16) & 0xFF), (short)(q >> 24)};
-    // (q - 32) * sc as q * sc + (-32 sc): one packed multiply-add per pair
+    // bytes 0, 1 and 2, 3 of q zero-extended to 16-bit lanes
+    const v2s x01 = __builtin_bit_cast(v2s, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+    const v2s x23 = __builtin_bit_cast(v2s, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+    // (q - 32) * sc + 128 as q * sc + (128 - 32 sc): one packed multiply-add per pair
     const v2s s2 = {(short)sc, (short)sc};
-    const v2s c2 = {(short)(-32 * sc), (short)(-32 * sc)};
-    const v2s w01 = x01 * s2 + c2, w23 = x23 * s2 + c2;
-    const v2s m7 = {127, 127};
-    const v2s l01 = w01 & m7, l23 = w23 & m7;
-    const v2s h01 = w01 >> 7, h23 = w23 >> 7;
-    lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, l23), __builtin_bit_cast(uint32_t, l01), 0x06040200u);
-    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
+    const v2s c2 = {(short)(128 - 32 * sc), (short)(128 - 32 * sc)};
+    const uint32_t w01 = __builtin_bit_cast(uint32_t, x01 * s2 + c2);
+    const uint32_t w23 = __builtin_bit_cast(uint32_t, x23 * s2 + c2);
+    lo = __builtin_amdgcn_perm(w23, w01, 0x06040200u) ^ 0x80808080u;
+    hi = __builtin_amdgcn_perm(w23, w01, 0x07050301u);
 }
 
 // 4 floats -> bf16 hi | bf16 lo (v = hi + lo to ~16 significant bits), packed as 16 bytes
@@ -197,7 +199,7 @@ __device__ __forceinline__ uint4 bf16_split4(const float* v) {
 template <int DT, class L, int TC = 2>
 __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint32_t lane, bool odd_sb, v4f* acc) {
     constexpr bool kQ4K = L::kQ4K;
-    constexpr int kShift = kQ4K ? 3 : 7;
+    constexpr int kShift = kQ4K ? 3 : 8;
     const uint32_t g = lane >> 4, li = lane & 15, h = g & 1;
     uint4 hdr[TC];
     Q4KScales qs[TC];
@@ -236,7 +238,8 @@ __device__ __forceinline__ void compute16(const uint8_t* S, uint32_t wave, uint3
                 const int sc = (int)(int8_t)(sw >> (8 * (2 * (c & 1) + h)));
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const uint32_t b = ((q4[j] >> (4 * h)) & 0x0F0F0F0Fu) | (((qhw >> (2 * j)) & 0x03030303u) << 4);
+                    const uint32_t qs = j < 2 ? qhw << (4 - 2 * j) : qhw >> (2 * j - 4);
+                    const uint32_t b = ((q4[j] >> (4 * h)) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
                     q6_digits(b, sc, p1[j], p0[j]);
                 }
             }
@@ -316,7 +319,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
     using L = KLay<DT, MT, NW>;
     constexpr int kCols = L::kCols;
     constexpr bool kQ4K = L::kQ4K;
-    constexpr int kShift = kQ4K ? 3 : 7;
+    constexpr int kShift = kQ4K ? 3 : 8;
     constexpr int kD = L::kD;
     constexpr int kRing = L::kRing;
     extern __shared__ __align__(16) uint8_t lds[];
