@@ -190,9 +190,11 @@ def test_matmul_config_shapes(orc, dev, dt, k, n, m):
 @pytest.mark.parametrize("m,n,k", [(64, 512, 4096), (130, 512, 4096), (300, 200, 768), (9, 129, 256),
                                    (257, 384, 1280), (16, 512, 7168), (24, 1000, 4096)])
 def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
-    """The int8-MFMA route (forced): ragged m and n against the 256 x 128
-    tiles, 1-28 super-blocks, and grids small enough to be split along K
-    (partial sums added in a second kernel)."""
+    """The int8-MFMA route (forced): ragged m and n against the tiles
+    (Q4_K up to 512 rows: the prefill kernel's 64- or 128-row by 256-column
+    tiles; Q6_K: the 256 x 128 tiled kernel), 1-28 super-blocks, and grids
+    small enough to be split along K (partial sums added in a second
+    kernel)."""
     from xn_amd.quantized import set_route
 
     rng = np.random.default_rng(8000 + dt + m + n + k)
