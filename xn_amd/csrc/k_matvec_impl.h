@@ -567,7 +567,14 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(WView w, AView a, const
     const uint32_t npass = (nchunks + 64 * CPL - 1) / (64 * CPL);
     const uint32_t ngroups = (w.n + R - 1) / R;
     const uint32_t gstride = gridDim.x * NW;
-    uint32_t g = blockIdx.x * NW + wave;
+    // The fused Q4_K kernel runs one workgroup per CU (launch_one): there its
+    // row groups go wave-major (g = wave * grid + block), so when they do not
+    // divide evenly every CU and SIMD gets the same share of the extra ones
+    // (4096 -> 14336: 56 rows per CU, where block-major order gave the first
+    // 128 workgroups 64 and the rest 48).  Grids of several workgroups per
+    // CU keep block-major order, which spreads them already.
+    constexpr bool kWaveMajor = FUSED && DT == XNQ_Q4K;
+    uint32_t g = kWaveMajor ? wave * gridDim.x + blockIdx.x : blockIdx.x * NW + wave;
 
     // Loads are unconditional (row and chunk clamped to the last valid one,
     // results past the end are never used): with no branches around them the
