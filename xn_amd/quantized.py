@@ -507,7 +507,8 @@ class capture:
 # -- lower-level entry points used by tests and the benchmark ------------------
 
 def set_route(route: int) -> None:
-    """0 = route by m, 1 = force the matvec kernel, 2 = force the MFMA kernel."""
+    """0 = route by m, 1 = force the matvec kernel, 2 = force the MFMA kernel,
+    3 = force the skinny MFMA kernel (m <= 64, Q4_K / Q6_K)."""
     check(_lib.load().xnq_set_route(int(route)))
 
 
