@@ -49,10 +49,11 @@ def one_hot_rows(m: int, k: int) -> np.ndarray:
     return x
 
 
-# auto routes: m = 16 the wavefront-split skinny kernel, 40 and 128 the
-# prefill kernel, 600 the tiled kernel; forced: 3 skinny (16- and 64-row
-# tiles), 2 the MFMA route
-@pytest.mark.parametrize("m,route", [(16, 0), (16, 3), (16, 2), (40, 3), (40, 0), (128, 0), (600, 0)])
+# auto routes: m = 1 the fused matvec (quantize in LDS), 16 the
+# wavefront-split skinny kernel, 40 and 128 the prefill kernel, 600 the
+# tiled kernel; forced: 1 the matvec, 3 skinny (16- and 64-row tiles), 2
+# the MFMA route
+@pytest.mark.parametrize("m,route", [(1, 0), (4, 1), (16, 0), (16, 3), (16, 2), (40, 3), (40, 0), (128, 0), (600, 0)])
 @pytest.mark.parametrize("term", ["main", "min"])
 @pytest.mark.parametrize("k", [256, 512])
 def test_q4k_digit_extremes(orc, dev, m, route, term, k):
