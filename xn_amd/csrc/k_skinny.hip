@@ -37,7 +37,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef short v2s __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
@@ -158,23 +157,6 @@ __device__ __forceinline__ void wait_younger_n(uint32_t kd, uint32_t younger) {
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
     const v2u16 s2 = {(unsigned short)s, (unsigned short)s};
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, d) * s2);
-}
-
-// Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale:
-// w = sc * (q - 32) in [-3968, 4096]; w + 128 = 256 * hi + u with u in
-// [0, 255], so w = 256 * hi + lo with hi = byte 1 of w + 128 (in [-15, 16])
-// and lo = u - 128 (byte 0 of w + 128 with its top bit flipped).
-__device__ __forceinline__ void q6_digits(uint32_t q, int sc, uint32_t& lo, uint32_t& hi) {
-    // bytes 0, 1 and 2, 3 of q zero-extended to 16-bit lanes
-    const v2s x01 = __builtin_bit_cast(v2s, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));
-    const v2s x23 = __builtin_bit_cast(v2s, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));
-    // (q - 32) * sc + 128 as q * sc + (128 - 32 sc): one packed multiply-add per pair
-    const v2s s2 = {(short)sc, (short)sc};
-    const v2s c2 = {(short)(128 - 32 * sc), (short)(128 - 32 * sc)};
-    const uint32_t w01 = __builtin_bit_cast(uint32_t, x01 * s2 + c2);
-    const uint32_t w23 = __builtin_bit_cast(uint32_t, x23 * s2 + c2);
-    lo = __builtin_amdgcn_perm(w23, w01, 0x06040200u) ^ 0x80808080u;
-    hi = __builtin_amdgcn_perm(w23, w01, 0x07050301u);
 }
 
 // 4 floats -> bf16 hi | bf16 lo (v = hi + lo to ~16 significant bits), packed as 16 bytes

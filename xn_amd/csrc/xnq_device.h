@@ -166,6 +166,25 @@ __device__ __forceinline__ void q6k_unpack(uint4 ql, uint2 qh, int* b) {
     b[7] = (int)(((ql.w >> 4) & M4) | (((qh.y >> 6) & M2) << 4));
 }
 
+// Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale,
+// for the int8 matrix cores (the skinny and tiled kernels):
+// w = sc * (q - 32) in [-3968, 4096]; w + 128 = 256 * hi + u with u in
+// [0, 255], so w = 256 * hi + lo with hi = byte 1 of w + 128 (in [-15, 16])
+// and lo = u - 128 (byte 0 of w + 128 with its top bit flipped).
+__device__ __forceinline__ void q6_digits(uint32_t q, int sc, uint32_t& lo, uint32_t& hi) {
+    typedef short s16x2 __attribute__((ext_vector_type(2)));
+    // bytes 0, 1 and 2, 3 of q zero-extended to 16-bit lanes
+    const s16x2 x01 = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+    const s16x2 x23 = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+    // (q - 32) * sc + 128 as q * sc + (128 - 32 sc): one packed multiply-add per pair
+    const s16x2 s2 = {(short)sc, (short)sc};
+    const s16x2 c2 = {(short)(128 - 32 * sc), (short)(128 - 32 * sc)};
+    const uint32_t w01 = __builtin_bit_cast(uint32_t, x01 * s2 + c2);
+    const uint32_t w23 = __builtin_bit_cast(uint32_t, x23 * s2 + c2);
+    lo = __builtin_amdgcn_perm(w23, w01, 0x06040200u) ^ 0x80808080u;
+    hi = __builtin_amdgcn_perm(w23, w01, 0x07050301u);
+}
+
 // Integer dot of one Q6K chunk: sc0 * sum_{16}(q6-32)*q8 + sc1 * (next 16),
 // using sum (q-32)*a = sum q*a - 32*sum a with the Q8K block sums.
 __device__ __forceinline__ int q6k_chunk_int(uint4 ql, uint2 qh, const int* a, int sc0, int sc1,
