@@ -191,7 +191,6 @@ constexpr int kTM = 2, kTN = 2;  // 32x32 tiles per wavefront (64 x 64)
 constexpr int kRing = 4;         // LDS ring slots (3 stages in flight + the current one)
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
 // LDS map (bytes).  Per stage: activation tile, raw weight chunks (Q6K: and
 // their high bits).  Per super-block (two buffers, by parity): d_a; Q4K: the
@@ -224,47 +223,6 @@ struct Lay {
     static constexpr int kBase1 = 2;              // 2 activation pieces
     static constexpr int kExtra1 = kQ4K ? 3 : 1;  // d_a, Q4K 2 x bsums
 };
-
-// global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
-// holds the LDS address lane 0 writes (lane i writes i * size beyond it).
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr),
-                 "v"(off), "s"(base)
-                 : "memory");
-}
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr),
-                 "v"(off), "s"(base)
-                 : "memory");
-}
-typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
-
-// bytes of d (each <= 15) times s (<= 7): every product is <= 105, so no
-// carry leaves its byte and one packed 16-bit multiply does all four
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
-    const v2u16 s2 = {(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, d) * s2);
-}
-
-// s_waitcnt vmcnt(N) for a compile-time N
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// 4 floats -> bf16 hi | bf16 lo (v = hi + lo to ~16 significant bits), packed as 16 bytes
-__device__ __forceinline__ uint4 bf16_split4(const float* v) {
-    v4bf h, l;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const __bf16 hb = (__bf16)v[t];
-        h[t] = hb;
-        l[t] = (__bf16)(v[t] - (float)hb);
-    }
-    const uint2 hu = __builtin_bit_cast(uint2, h), lu = __builtin_bit_cast(uint2, l);
-    return make_uint4(hu.x, hu.y, lu.x, lu.y);
-}
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_t m, uint32_t sb_per_split,
@@ -415,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
 #pragma unroll
                         for (int t = 0; t < 4; t++)
                             v[t] = -da * (float)((int)(int16_t)(prs[t] & 0xffffu) + (int)(int16_t)(prs[t] >> 16));
-                        *sp = bf16_split4(v);
+                        *sp = bf16_hilo4(v);
                     }
                 }
                 return;
@@ -451,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                         v[t] = dm * (float)mn2;
                     }
                     *reinterpret_cast<uint4*>(epi + L::kEB + (((cw * 2 + (lane >> 5)) * 2 + bc) * 32 + (lane & 31)) * 16) =
-                        bf16_split4(v);
+                        bf16_hilo4(v);
                 }
             } else {
                 const uint2 qh = *reinterpret_cast<const uint2*>(raw + L::kQSlot + (bc * kBN + col) * 16 + bc * 8);

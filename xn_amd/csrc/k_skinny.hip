@@ -37,9 +37,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
 // LDS slot of one super-block (byte offsets).  R = 16 activation rows for
 // MT == 0 (16-row tiles), else 32 * MT; C = 32 * NW columns.
@@ -107,24 +105,6 @@ struct KLay {
     }
 };
 
-// global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
-// holds the LDS address lane 0 writes (lane i writes i * size beyond it).
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr),
-                 "v"(off), "s"(base)
-                 : "memory");
-}
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr),
-                 "v"(off), "s"(base)
-                 : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Wait until at most `younger` super-blocks' DMA (KD instructions each) are
 // outstanding, younger <= Y (wavefront-uniform).
 template <int KD, int Y>
@@ -153,24 +133,6 @@ __device__ __forceinline__ void wait_younger_n(uint32_t kd, uint32_t younger) {
     }
 }
 
-// bytes of d (each <= 15) times s (<= 7): one packed 16-bit multiply
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
-    const v2u16 s2 = {(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, d) * s2);
-}
-
-// 4 floats -> bf16 hi | bf16 lo (v = hi + lo to ~16 significant bits), packed as 16 bytes
-__device__ __forceinline__ uint4 bf16_split4(const float* v) {
-    v4bf h, l;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const __bf16 hb = (__bf16)v[t];
-        h[t] = hb;
-        l[t] = (__bf16)(v[t] - (float)hb);
-    }
-    const uint2 hu = __builtin_bit_cast(uint2, h), lu = __builtin_bit_cast(uint2, l);
-    return make_uint4(hu.x, hu.y, lu.x, lu.y);
-}
 
 // One super-block of a 16-row tile (m <= 16) for wavefront `wave`'s 16 * TC
 // columns, as TC 16-column tiles on v_mfma_i32_16x16x64_i8: lane l holds
@@ -486,7 +448,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
             float v[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) v[u] = dm * (float)((mw >> (8 * u)) & 0xffu);
-            const uint4 bv = bf16_split4(v);
+            const uint4 bv = bf16_hilo4(v);
             bh8 = __builtin_bit_cast(v8bf, make_uint4(bv.x, bv.y, bv.x, bv.y));
             bl8 = __builtin_bit_cast(v8bf, make_uint4(bv.z, bv.w, bv.z, bv.w));
         }
@@ -512,7 +474,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_kernel(WGroup G, SkOut O, AVie
 #pragma unroll
                 for (int u = 0; u < 4; u++)
                     v[u] = -da * (float)((int)(int16_t)(prs[u] & 0xffffu) + (int)(int16_t)(prs[u] >> 16));
-                const v8bf a8 = __builtin_bit_cast(v8bf, bf16_split4(v));
+                const v8bf a8 = __builtin_bit_cast(v8bf, bf16_hilo4(v));
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bh8, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8, bl8, acc[t], 0, 0, 0);
             }

@@ -166,6 +166,36 @@ __device__ __forceinline__ void q6k_unpack(uint4 ql, uint2 qh, int* b) {
     b[7] = (int)(((ql.w >> 4) & M4) | (((qh.y >> 6) & M2) << 4));
 }
 
+// ---- LDS DMA (the int8-MFMA kernels) ---------------------------------------
+
+// global_load_lds: uniform 64-bit base + 32-bit per-lane byte offset; m0
+// holds the LDS address lane 0 writes (lane i writes i * size beyond it).
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr),
+                 "v"(off), "s"(base)
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr),
+                 "v"(off), "s"(base)
+                 : "memory");
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// bytes of d (each <= 15) times s (<= 7): every product is <= 105, so no
+// carry leaves its byte and one packed 16-bit multiply does all four
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t d, uint32_t s) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 s2 = {(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, d) * s2);
+}
+
 // Q6K digit planes of 4 six-bit values (bytes of q) times a signed scale,
 // for the int8 matrix cores (the skinny and tiled kernels):
 // w = sc * (q - 32) in [-3968, 4096]; w + 128 = 256 * hi + u with u in
