@@ -224,7 +224,7 @@ struct Lay {
     static constexpr int kExtra1 = kQ4K ? 3 : 1;  // d_a, Q4K 2 x bsums
 };
 
-template <int DT>
+template <int DT, bool PART>
 __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_t m, uint32_t sb_per_split,
                                                        float* __restrict__ y, size_t split_stride) {
     using L = Lay<DT>;
@@ -303,9 +303,13 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         }
     };
 
-    // The main loop, specialised per wavefront group (G = 0: weights, 1: activation side data).
-    auto run = [&](auto gc) {
+    // The main loop, specialised per wavefront group (G = 0: weights, 1:
+    // activation side data) and by whether the wavefront's 64 rows hold any
+    // row below m (MF; without, its MFMAs and epilogues are left out and it
+    // only fetches and expands its share for the others).
+    auto run = [&](auto gc, auto mfc) {
         constexpr int G = decltype(gc)::value;
+        constexpr bool MF = decltype(mfc)::value;
         constexpr int kBase = G == 0 ? L::kBase0 : L::kBase1;
         constexpr int kExtra = G == 0 ? L::kExtra0 : L::kExtra1;
         constexpr int kParts = kBase + kExtra;
@@ -324,30 +328,38 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         const uint32_t nstage = 4 * nsb;
 
         // DMA instruction p of stage st (parts past kBase only at a super-block's first stage)
+        // (the LDS addresses are wavefront-uniform; readfirstlane states it
+        // where the group/row specialisation hides it from the compiler)
+        auto dma16u = [](const void* base, uint32_t off, uint32_t lds_addr) {
+            dma16(base, off, PART ? __builtin_amdgcn_readfirstlane(lds_addr) : lds_addr);
+        };
+        auto dma4u = [](const void* base, uint32_t off, uint32_t lds_addr) {
+            dma4(base, off, PART ? __builtin_amdgcn_readfirstlane(lds_addr) : lds_addr);
+        };
         auto issue_part = [&](uint32_t st, int p) {
             const uint32_t slot = st % kRing, sb = st >> 2;
             const uint32_t epi = lbase + L::kOffEpi + (sb & 1) * L::kEpi;
             if (p < 2) {
                 // activation piece t = 2*wave + p: (ks, h, 64-row block)
                 const uint32_t t = 2 * wave + p, ks = t >> 3, h = (t >> 2) & 1, rb = t & 3;
-                dma16(t_q + (size_t)rblk(rb) * 64 * K + st * 4096 + (ks * 2 + h) * 1024, lane16,
+                dma16u(t_q + (size_t)rblk(rb) * 64 * K + st * 4096 + (ks * 2 + h) * 1024, lane16,
                       lbase + L::kOffA + slot * L::kASlot + ((ks * 2 + h) * kBM + rb * 64) * 16);
                 return;
             }
             if (G == 0) {
                 const uint32_t raw = lbase + L::kOffRaw + slot * L::kRawSlot + (bc * kBN + cw * 64) * 16;
                 // chunk 2 * (st & 3) + bc of super-block st >> 2
-                if (p == 2) dma16(wq + bc * 16 + st * 32, q_lane, raw);
-                if (!kQ4K && p == 3) dma16(wh + st * 16, q_lane >> 1, raw + L::kQSlot);  // qh of chunks 2st, 2st+1
-                if (p == kBase) dma16(ws + sb * 2048, lc * 16, epi + L::kEHdr + cw * 64 * 16);
+                if (p == 2) dma16u(wq + bc * 16 + st * 32, q_lane, raw);
+                if (!kQ4K && p == 3) dma16u(wh + st * 16, q_lane >> 1, raw + L::kQSlot);  // qh of chunks 2st, 2st+1
+                if (p == kBase) dma16u(ws + sb * 2048, lc * 16, epi + L::kEHdr + cw * 64 * 16);
                 if (!kQ4K && p == kBase + 1)
-                    dma4(wd + ((sb0 + sb) >> 1) * 512, lc * 4, epi + L::kEB + cw * 64 * 4);
+                    dma4u(wd + ((sb0 + sb) >> 1) * 512, lc * 4, epi + L::kEB + cw * 64 * 4);
             } else {
                 if (p == kBase)
-                    dma4(t_d + ((size_t)rblk(gw) * nsb_all + sb) * 256, lane4, epi + L::kEDa + 64 * gw * 4);
+                    dma4u(t_d + ((size_t)rblk(gw) * nsb_all + sb) * 256, lane4, epi + L::kEDa + 64 * gw * 4);
                 if (kQ4K && p > kBase) {
                     const uint32_t i = p - kBase - 1;  // row 64*gw + 32*i + lane%32, half lane/32
-                    dma16(t_s + (((size_t)rblk(gw) * nsb_all + sb) * 2 + i) * 1024, lane16,
+                    dma16u(t_s + (((size_t)rblk(gw) * nsb_all + sb) * 2 + i) * 1024, lane16,
                           epi + L::kESum + (64 * gw + 32 * i) * 32);
                 }
             }
@@ -458,18 +470,21 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
             };
             {
                 v4i av[kTM], bv[2][kTN];
+                if constexpr (MF) {
 #pragma unroll
-                for (int i = 0; i < kTM; i++) av[i] = a_frag(0, i);
+                    for (int i = 0; i < kTM; i++) av[i] = a_frag(0, i);
 #pragma unroll
-                for (int p = 0; p < 2; p++)
+                    for (int p = 0; p < 2; p++)
 #pragma unroll
-                    for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(0, p, j);
+                        for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(0, p, j);
+                }
 #pragma unroll
                 for (int i = 0; i < kTM; i++)
 #pragma unroll
                     for (int j = 0; j < kTN; j++) {
                         const int k = (i * kTN + j) * 2;
-                        if (t == 0) {
+                        if constexpr (!MF) {
+                        } else if (t == 0) {
                             hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[0][j], v16i{}, 0, 0, 0);
                             lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[1][j], v16i{}, 0, 0, 0);
                         } else {
@@ -483,20 +498,24 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
             if (kExpand) wait_vm<kC2 + kC3>();
             {
                 v4i av[kTM], bv[2][kTN];
+                if constexpr (MF) {
 #pragma unroll
-                for (int i = 0; i < kTM; i++) av[i] = a_frag(1, i);
+                    for (int i = 0; i < kTM; i++) av[i] = a_frag(1, i);
 #pragma unroll
-                for (int p = 0; p < 2; p++)
+                    for (int p = 0; p < 2; p++)
 #pragma unroll
-                    for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(1, p, j);
+                        for (int j = 0; j < kTN; j++) bv[p][j] = b_frag(1, p, j);
+                }
                 if (kExpand) expand(s + 1, std::integral_constant<bool, ((t + 1) & 3) == 0>{});
+                if constexpr (MF) {
 #pragma unroll
-                for (int i = 0; i < kTM; i++)
+                    for (int i = 0; i < kTM; i++)
 #pragma unroll
-                    for (int j = 0; j < kTN; j++) {
-                        hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[0][j], hi[i][j], 0, 0, 0);
-                        lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[1][j], lo[i][j], 0, 0, 0);
-                    }
+                        for (int j = 0; j < kTN; j++) {
+                            hi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[0][j], hi[i][j], 0, 0, 0);
+                            lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[1][j], lo[i][j], 0, 0, 0);
+                        }
+                }
                 // interleave: LDS reads first, then one MFMA per few VALU
                 // instructions of the expansion, then its LDS writes
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
@@ -507,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
                 }
                 __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
             }
-            if (t == 3) {
+            if (MF && t == 3) {
 #pragma unroll
                 for (int i = 0; i < kTM; i++)
 #pragma unroll
@@ -544,10 +563,21 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         stage(nsb - 1, I2{}, std::true_type{});
         stage(nsb - 1, I3{}, std::true_type{});
     };
-    if (wave < 4)
-        run(std::integral_constant<int, 0>{});
-    else
-        run(std::integral_constant<int, 1>{});
+    // wavefront-uniform: does this wavefront's 64-row band hold a row below m
+    // (PART: the launch has a last row tile at most half full; the variant
+    // without MFMAs costs the full tiles a few spilled registers, so only
+    // such launches carry it)
+    const bool rows = !PART || __builtin_amdgcn_readfirstlane(m0 + wm * 64 < m ? 1u : 0u) != 0;
+    if (!PART) {
+        if (wave < 4) run(std::integral_constant<int, 0>{}, std::true_type{});
+        else run(std::integral_constant<int, 1>{}, std::true_type{});
+    } else if (wave < 4) {
+        if (rows) run(std::integral_constant<int, 0>{}, std::true_type{});
+        else run(std::integral_constant<int, 0>{}, std::false_type{});
+    } else {
+        if (rows) run(std::integral_constant<int, 1>{}, std::true_type{});
+        else run(std::integral_constant<int, 1>{}, std::false_type{});
+    }
 
     // ---- write the tile ----
 #pragma unroll
@@ -564,11 +594,11 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         }
 }
 
-template <int DT>
+template <int DT, bool PART>
 hipError_t launch_dt(const WView& w, const AView& a, size_t m, uint32_t splits, float* y, float* partial,
                      hipStream_t s) {
     {
-        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(qmm_kernel<DT>), Lay<DT>::kLds);
+        const hipError_t e = set_max_lds(reinterpret_cast<const void*>(qmm_kernel<DT, PART>), Lay<DT>::kLds);
         if (e != hipSuccess) return e;
     }
     const uint32_t nsb = w.k / 256;
@@ -576,7 +606,7 @@ hipError_t launch_dt(const WView& w, const AView& a, size_t m, uint32_t splits, 
     splits = (nsb + per - 1) / per;  // every split non-empty
     const dim3 grid((w.n + kBN - 1) / kBN, (unsigned)((m + kBM - 1) / kBM), splits);
     float* out = splits > 1 ? partial : y;
-    hipLaunchKernelGGL(qmm_kernel<DT>, grid, dim3(kThreads), Lay<DT>::kLds, s, w, a, (uint32_t)m, per, out,
+    hipLaunchKernelGGL((qmm_kernel<DT, PART>), grid, dim3(kThreads), Lay<DT>::kLds, s, w, a, (uint32_t)m, per, out,
                        splits > 1 ? m * (size_t)w.n : (size_t)0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
@@ -609,8 +639,19 @@ hipError_t launch_mfma(const WView& w, const AView& a, size_t m, uint32_t splits
     if (!a.tile || (size_t)a.T.rbs * 64 < m || a.k != w.k) return hipErrorInvalidValue;
     if (splits > 1 && !partial) splits = 1;
     if (prefill_supported(w.dtype, m, w.n, w.k)) return launch_prefill(w, a, m, splits, y, partial, s);
-    if (w.dtype == XNQ_Q4K) return launch_dt<XNQ_Q4K>(w, a, m, splits, y, partial, s);
-    if (w.dtype == XNQ_Q6K) return launch_dt<XNQ_Q6K>(w, a, m, splits, y, partial, s);
+    // a last row tile at most half full leaves its wavefronts 4-7 without
+    // rows: the PART kernel drops their MFMAs (Q6_K 4096 -> 14336, µs, one
+    // box: m = 65 46 -> 43, 128 49 -> 45; Q4_K m = 600 136 -> 121; full tiles
+    // keep the kernel without the branch: 256 51 against 53, 512 75-78
+    // against 80-81)
+    const size_t tail = m % kBM;
+    const bool part = tail != 0 && tail <= kBM / 2;
+    if (w.dtype == XNQ_Q4K)
+        return part ? launch_dt<XNQ_Q4K, true>(w, a, m, splits, y, partial, s)
+                    : launch_dt<XNQ_Q4K, false>(w, a, m, splits, y, partial, s);
+    if (w.dtype == XNQ_Q6K)
+        return part ? launch_dt<XNQ_Q6K, true>(w, a, m, splits, y, partial, s)
+                    : launch_dt<XNQ_Q6K, false>(w, a, m, splits, y, partial, s);
     return hipErrorNotSupported;
 }
 
