@@ -188,13 +188,16 @@ def test_matmul_config_shapes(orc, dev, dt, k, n, m):
 
 @pytest.mark.parametrize("dt", [Q4K, Q6K])
 @pytest.mark.parametrize("m,n,k", [(64, 512, 4096), (130, 512, 4096), (300, 200, 768), (9, 129, 256),
-                                   (257, 384, 1280), (16, 512, 7168), (24, 1000, 4096)])
+                                   (257, 384, 1280), (16, 512, 7168), (24, 1000, 4096), (128, 384, 512),
+                                   (129, 384, 512), (640, 300, 512)])
 def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
     """The int8-MFMA route (forced): ragged m and n against the tiles
     (Q4_K up to 512 rows: the prefill kernel's 64- or 128-row by 256-column
-    tiles; Q6_K: the 256 x 128 tiled kernel), 1-28 super-blocks, and grids
-    small enough to be split along K (partial sums added in a second
-    kernel)."""
+    tiles; Q6_K and Q4_K past 512 rows: the 256 x 128 tiled kernel, whose
+    instance for a last row tile at most half full drops the MFMAs of the
+    wavefronts past m: tails of 128 (that instance) and 129 (the other)),
+    1-28 super-blocks, and grids small enough to be split along K (partial
+    sums added in a second kernel)."""
     from xn_amd.quantized import set_route
 
     rng = np.random.default_rng(8000 + dt + m + n + k)
