@@ -781,11 +781,6 @@ __global__ __launch_bounds__(NW * 64) void group_kernel(WGroup G, const float* _
     }
 }
 
-inline int env_int(const char* name, int dflt) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : dflt;
-}
-
 // Occupancy (workgroups per CU) of one kernel at one LDS size, cached.
 inline int wg_per_cu(const void* fn, int threads, uint32_t lds_bytes, int* num_cu) {
     static std::mutex mu;
@@ -825,9 +820,8 @@ hipError_t launch_one(const WView& w, const AView& a, const float* x, uint32_t m
     // the fused Q4_K kernel runs one 16-wavefront workgroup per CU: each CU
     // then quantizes the row once, not twice (4096 -> 14336 step 9.27 ->
     // 8.82 us); Q4_0 (7.7 -> 9.4) and Q6_K (69.1 -> 69.7 on the lm_head)
-    // keep the full occupancy.  XNQ_MV_FUSED_OCC sets it (tuning).
-    static const int fused_occ = env_int("XNQ_MV_FUSED_OCC", 0);
-    const int wg_cu = !FUSED ? occ : fused_occ > 0 ? std::min(fused_occ, occ) : DT == XNQ_Q4K ? 1 : occ;
+    // keep the full occupancy.
+    const int wg_cu = FUSED && DT == XNQ_Q4K ? 1 : occ;
     const uint32_t cap = (uint32_t)(wg_cu * ncu);
     const uint32_t grid = need < cap ? need : cap;
     hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, w, a, x, m0, mc, y);
@@ -843,9 +837,8 @@ hipError_t launch_group_one(const WGroup& g, const float* x, hipStream_t s) {
     int ncu = 1;
     const int occ = wg_per_cu(reinterpret_cast<const void*>(fn), NW * kWave, lds, &ncu);
     const uint32_t need = (g.rows + R * NW - 1) / (R * NW);
-    static const bool one_shot = env_int("XNQ_GROUP_ONE_SHOT", 0) != 0;
     const uint32_t cap = (uint32_t)(occ * ncu);
-    const uint32_t grid = one_shot || need < cap ? need : cap;
+    const uint32_t grid = need < cap ? need : cap;
     hipLaunchKernelGGL(fn, dim3(grid), dim3(NW * kWave), lds, s, g, x);
     return hipGetLastError();
 }
@@ -882,91 +875,51 @@ hipError_t launch_group_r(int cpl, const WGroup& g, const float* x, hipStream_t 
 // the weight loads issued ahead of the quantizer, that measured fastest
 // (decode step 1432 -> 1376 us against two rows per wavefront, which uses
 // fewer workgroups and so quantizes the activation fewer times).
-// XNQ_MV_STREAM_ROWS=2 forces two rows (tuning).  Returns
-// hipErrorNotSupported for a GATE shape past the register bound.
+// Returns hipErrorNotSupported for a GATE shape past the register bound.
 template <int DT, bool GATE>
 hipError_t launch_group(const WGroup& g, const float* x, hipStream_t s) {
     const uint32_t nchunks = g.w[0].k / 32;
     const int cpl = (int)std::min<uint32_t>(8, (nchunks + 63) / 64);
     if (GATE && cpl > 5) return hipErrorNotSupported;
-    static const int forced = env_int("XNQ_MV_STREAM_ROWS", 0);
-    int r = forced == 2 ? 2 : 1;
-    if (cpl > (GATE ? 2 : 5)) r = 1;
-    if (r == 1) return launch_group_r<DT, 1, GATE>(cpl, g, x, s);
-    return launch_group_r<DT, 2, GATE>(cpl, g, x, s);
+    return launch_group_r<DT, 1, GATE>(cpl, g, x, s);
 }
 
 inline int pick_cpl(uint32_t nchunks) {
     return nchunks <= 64 ? 1 : nchunks <= 128 ? 2 : nchunks <= 256 ? 4 : 8;
 }
 
-// Decode kernels read a quantized workspace (4 wavefronts per workgroup at
-// one row of K <= 8192, else 8; many workgroups); the fused m == 1 kernel
-// quantizes in LDS and so uses 16-wavefront workgroups to share that work.
-template <int DT, int MB, bool FUSED>
-hipError_t launch_cpl(int R, int cpl, const WView& w, const AView& a, const float* x, uint32_t m0,
-                      uint32_t mc, float* y, hipStream_t s) {
-    constexpr int NW = FUSED ? 16 : 4;
-#define XNQ_MV(RR, CC)                                                          \
-    if (R == RR && cpl == CC) return launch_one<DT, MB, RR, CC, NW, FUSED>(w, a, x, m0, mc, y, s);
-    if constexpr (MB == 1 && FUSED) {
-        static const int fnw = env_int("XNQ_MV_FUSED_NW", 16);
-        if (R == 1 && fnw == 4) {
-            if (cpl == 1) return launch_one<DT, MB, 1, 1, 4, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 2) return launch_one<DT, MB, 1, 2, 4, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 4) return launch_one<DT, MB, 1, 4, 4, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 8) return launch_one<DT, MB, 1, 8, 4, FUSED>(w, a, x, m0, mc, y, s);
-        }
-        if (R == 1 && fnw == 8) {
-            if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 8) return launch_one<DT, MB, 1, 8, 8, FUSED>(w, a, x, m0, mc, y, s);
-        }
+// One weight row per wavefront (more rows per wavefront cost occupancy and
+// measured slower for every shape).  Wavefronts per workgroup: the fused
+// kernels 16 (the workgroup shares the row's quantization); the workspace
+// kernels at one row 8 for rows of 8 chunks per lane (K > 8192: 14336 ->
+// 4096 Q4_K 8.25 against 8.87 us, Q4_0 7.97 against 8.97) and 4 for shorter
+// rows (8192 -> 28672: 22.5 against 23.3), and at 2..8 rows 8, which stage
+// the rows into LDS half as often (4096 -> 14336 at m = 4: 11.9 against
+// 12.5 us).
+template <int DT, int MB, int NW, bool FUSED>
+hipError_t launch_by_cpl(int cpl, const WView& w, const AView& a, const float* x, uint32_t m0, uint32_t mc,
+                         float* y, hipStream_t s) {
+    switch (cpl) {
+    case 1: return launch_one<DT, MB, 1, 1, NW, FUSED>(w, a, x, m0, mc, y, s);
+    case 2: return launch_one<DT, MB, 1, 2, NW, FUSED>(w, a, x, m0, mc, y, s);
+    case 4: return launch_one<DT, MB, 1, 4, NW, FUSED>(w, a, x, m0, mc, y, s);
+    case 8: return launch_one<DT, MB, 1, 8, NW, FUSED>(w, a, x, m0, mc, y, s);
     }
-    if constexpr (MB == 1 && !FUSED) {
-        // rows of 8 chunks per lane (K > 8192): 8-wavefront workgroups
-        // (14336 -> 4096 Q4_K 8.25 against 8.87 us, Q4_0 7.97 against 8.97);
-        // shorter rows keep 4 (8192 -> 28672: 22.5 against 23.3).
-        // XNQ_MV_NW1=4|8 forces it (tuning).
-        static const int nw1 = env_int("XNQ_MV_NW1", 0);
-        if (R == 1 && (nw1 == 8 || (nw1 == 0 && cpl == 8))) {
-            if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
-            if (cpl == 8) return launch_one<DT, MB, 1, 8, 8, FUSED>(w, a, x, m0, mc, y, s);
-        }
-    }
-    if constexpr (MB == 1) {
-        XNQ_MV(1, 1) XNQ_MV(2, 1) XNQ_MV(4, 1) XNQ_MV(1, 2) XNQ_MV(2, 2) XNQ_MV(4, 2)
-        XNQ_MV(1, 4) XNQ_MV(2, 4) XNQ_MV(1, 8)
-    } else {
-        // 2..8 rows: 8-wavefront workgroups stage the rows into LDS half as
-        // often as 4-wavefront ones (4096 -> 14336 at m = 4: 11.9 against
-        // 12.5 us); XNQ_MV_NW_MB=4 restores 4 (tuning)
-        if constexpr (!FUSED) {
-            static const int nw = env_int("XNQ_MV_NW_MB", 8);
-            if (R == 1 && nw == 8) {
-                if (cpl == 1) return launch_one<DT, MB, 1, 1, 8, FUSED>(w, a, x, m0, mc, y, s);
-                if (cpl == 2) return launch_one<DT, MB, 1, 2, 8, FUSED>(w, a, x, m0, mc, y, s);
-                if (cpl == 4) return launch_one<DT, MB, 1, 4, 8, FUSED>(w, a, x, m0, mc, y, s);
-                if (cpl == 8) return launch_one<DT, MB, 1, 8, 8, FUSED>(w, a, x, m0, mc, y, s);
-            }
-        }
-        XNQ_MV(1, 1) XNQ_MV(1, 2) XNQ_MV(1, 4) XNQ_MV(1, 8)
-    }
-#undef XNQ_MV
     return hipErrorInvalidValue;
 }
 
-// Rows per wavefront.  One row per wavefront measured fastest for every
-// shape so far (more rows per wave cost occupancy); XNQ_MV_ROWS=2|4 is a
-// tuning override.
-inline int pick_rows(uint32_t n, int cpl) {
-    (void)n;
-    static const int forced = env_int("XNQ_MV_ROWS", 0);
-    if ((forced == 2 || forced == 4) && forced * cpl <= 8) return forced;
-    return 1;
+template <int DT, int MB, bool FUSED>
+hipError_t launch_cpl(int cpl, const WView& w, const AView& a, const float* x, uint32_t m0, uint32_t mc, float* y,
+                      hipStream_t s) {
+    if constexpr (FUSED) return launch_by_cpl<DT, MB, 16, true>(cpl, w, a, x, m0, mc, y, s);
+    if constexpr (MB > 1) return launch_by_cpl<DT, MB, 8, false>(cpl, w, a, x, m0, mc, y, s);
+    if (cpl == 8) return launch_one<DT, 1, 1, 8, 8, false>(w, a, x, m0, mc, y, s);
+    switch (cpl) {
+    case 1: return launch_one<DT, 1, 1, 1, 4, false>(w, a, x, m0, mc, y, s);
+    case 2: return launch_one<DT, 1, 1, 2, 4, false>(w, a, x, m0, mc, y, s);
+    case 4: return launch_one<DT, 1, 1, 4, 4, false>(w, a, x, m0, mc, y, s);
+    }
+    return hipErrorInvalidValue;
 }
 
 // y[m x n] for all m rows, in launches of up to 8 rows: `fused` nonzero
@@ -985,8 +938,7 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
     for (size_t m0 = 0; m0 < m; m0 += gmax) {
         const uint32_t mc = (uint32_t)((m - m0) < (size_t)gmax ? (m - m0) : (size_t)gmax);
         hipError_t e;
-        static const bool legacy = env_int("XNQ_MV_LEGACY", 0) != 0;
-        if (mc == 1 && m == 1 && fused == kFusedOneShot && !legacy) {
+        if (mc == 1 && m == 1 && fused == kFusedOneShot) {
             WGroup g{};
             g.w[0] = w;
             g.y[0] = y;
@@ -995,15 +947,15 @@ hipError_t launch_dtype(const WView& w, const AView& a, const float* x, size_t m
             g.rows = w.n;
             e = launch_group<DT, false>(g, x, s);
         } else if (fused) {
-            if (mc == 1) e = launch_cpl<DT, 1, true>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
-            else if (mc == 2) e = launch_cpl<DT, 2, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
-            else if (mc <= 4) e = launch_cpl<DT, 4, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
-            else e = launch_cpl<DT, 8, true>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            if (mc == 1) e = launch_cpl<DT, 1, true>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc == 2) e = launch_cpl<DT, 2, true>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc <= 4) e = launch_cpl<DT, 4, true>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else e = launch_cpl<DT, 8, true>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
         } else {
-            if (mc == 1) e = launch_cpl<DT, 1, false>(pick_rows(w.n, cpl), cpl, w, a, x, (uint32_t)m0, mc, y, s);
-            else if (mc == 2) e = launch_cpl<DT, 2, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
-            else if (mc <= 4) e = launch_cpl<DT, 4, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
-            else e = launch_cpl<DT, 8, false>(1, cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            if (mc == 1) e = launch_cpl<DT, 1, false>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc == 2) e = launch_cpl<DT, 2, false>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else if (mc <= 4) e = launch_cpl<DT, 4, false>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
+            else e = launch_cpl<DT, 8, false>(cpl, w, a, x, (uint32_t)m0, mc, y, s);
         }
         if (e != hipSuccess) return e;
     }

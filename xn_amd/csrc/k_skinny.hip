@@ -711,15 +711,9 @@ static bool wk_eight_waves(size_t tiles32, size_t m) { return m <= 8 && 2 * tile
 // wavefront, K = 14336 was slower (Q4_K 14336 -> 4096 19.4 -> 22.3: half the
 // CUs, 14 super-blocks per wavefront), and so are more tiles, which take
 // extra rounds (the gate/up pair 25.5 -> 29.9, 8192 -> 28672 40.1 -> 44.2,
-// the Q6_K lm_head 125 -> 164).  XNQ_SKINNY_WK=0 turns it off, 2 forces it
-// for every 16-row launch (tuning).
+// the Q6_K lm_head 125 -> 164).
 static bool skinny_wk(uint32_t dtype, size_t tiles32, size_t k) {
-    static const int mode = [] {
-        const char* e = getenv("XNQ_SKINNY_WK");
-        return e ? atoi(e) : 1;
-    }();
-    if (mode == 2) return true;
-    if (mode == 0 || tiles32 > 512) return false;
+    if (tiles32 > 512) return false;
     // the one-tile form at any K while its workgroups fit one round at two
     // per CU (Q6_K 14336 -> 4096, 128 tiles: 25.3 -> 21.0 µs; Q4_K
     // 14336 -> 4096 18.9 -> 18.2), else K <= 4096
@@ -773,13 +767,8 @@ hipError_t launch_skinny_dt(const WGroup& G, const AView& a, size_t m, uint32_t 
 // splits); above, 8 (two per SIMD, so one wavefront's expansion overlaps the
 // other's waits) above 32 rows (two row tiles: 4096 x 4096 at m = 64 13.8
 // against 16.2 us) or where the column tiles still cover the CUs with K
-// split at most 4 ways, else 4.  XNQ_SKINNY_NW=4|8 forces it (tuning).
+// split at most 4 ways, else 4.
 static int skinny_waves(size_t m, size_t n, size_t k) {
-    static const int forced = [] {
-        const char* e = getenv("XNQ_SKINNY_NW");
-        return e ? atoi(e) : 0;
-    }();
-    if (forced == 4 || forced == 8) return forced;
     if (m <= 16) return 4;
     if (m > 32) return 8;
     const size_t tiles8 = (n + 255) / 256, nsb = k / 256;
@@ -793,27 +782,12 @@ uint32_t skinny_splits(size_t m, size_t n, size_t k) {
     // wavefront-split kernel does not take: many column tiles) gained from
     // the second workgroup per CU (8192 -> 28672 at m = 16 40.2 -> 37.9 us,
     // the Q6_K lm_head 116 -> 111); the 32-row tiles keep one.
-    // XNQ_SKINNY_WG_TARGET overrides the target (tuning).
     const size_t tiles = (n + 32 * skinny_waves(m, n, k) - 1) / (32 * skinny_waves(m, n, k));
     const size_t nsb = k / 256;
-    static const size_t forced_target = [] {
-        const char* e = getenv("XNQ_SKINNY_WG_TARGET");
-        return e && atoi(e) > 0 ? (size_t)atoi(e) : (size_t)0;
-    }();
-    const size_t target = forced_target ? forced_target : m <= 16 ? 512 : 256;
+    const size_t target = m <= 16 ? 512 : 256;
     size_t splits = target / tiles;
     if (splits > nsb / 2) splits = nsb / 2;
     return splits < 1 ? 1u : (uint32_t)splits;
-}
-
-// 16-row tiles on the 16x16x64 matrix-core op for m <= 16 (XNQ_SKINNY16=0
-// keeps the 32-row tiles; tuning)
-static bool skinny16() {
-    static const bool on = [] {
-        const char* e = getenv("XNQ_SKINNY16");
-        return !e || atoi(e) != 0;
-    }();
-    return on;
 }
 
 bool skinny_supported(uint32_t dtype, size_t m, size_t n, size_t k) {
@@ -835,20 +809,18 @@ hipError_t launch_skinny_group(const WGroup& G, const AView& a, size_t m, uint32
     const bool w8 = skinny_waves(m, n, G.w[0].k) == 8;
 #define XNQ_SK(DT)                                                                                   \
     if (G.w[0].dtype == DT) {                                                                        \
-        if (m <= 16 && skinny16() && skinny_wk(DT, tiles32, G.w[0].k) && (!silu || partial))       \
+        if (m <= 16 && skinny_wk(DT, tiles32, G.w[0].k) && (!silu || partial))                     \
             return wk_one_tile(DT, tiles32)                                                          \
                        ? (wk_eight_waves(tiles32, m)                                                  \
                               ? launch_skinny_wk<DT, 8, 2, 1>(G, a, m, partial, silu, s, next, next_img) \
                               : launch_skinny_wk<DT, 4, 2, 1>(G, a, m, partial, silu, s, next, next_img)) \
                        : launch_skinny_wk<DT, 4, 2, 2>(G, a, m, partial, silu, s, next, next_img);     \
-        if (m <= 16 && skinny16())                                                                 \
-            return w8 ? launch_skinny_dt<DT, 0, 8>(G, a, m, splits, partial, silu, s, next, next_img)               \
-                      : launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s, next, next_img);              \
+        /* 16-row tiles on the 16x16x64 op (four wavefronts) up to 16 rows */                      \
+        if (m <= 16) return launch_skinny_dt<DT, 0, 4>(G, a, m, splits, partial, silu, s, next, next_img); \
         if (m <= 32)                                                                                 \
             return w8 ? launch_skinny_dt<DT, 1, 8>(G, a, m, splits, partial, silu, s, next, next_img)               \
                       : launch_skinny_dt<DT, 1, 4>(G, a, m, splits, partial, silu, s, next, next_img);              \
-        return w8 ? launch_skinny_dt<DT, 2, 8>(G, a, m, splits, partial, silu, s, next, next_img)                   \
-                  : launch_skinny_dt<DT, 2, 4>(G, a, m, splits, partial, silu, s, next, next_img);                  \
+        return launch_skinny_dt<DT, 2, 8>(G, a, m, splits, partial, silu, s, next, next_img);                       \
     }
     XNQ_SK(XNQ_Q4K)
     XNQ_SK(XNQ_Q6K)
