@@ -327,15 +327,15 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(WView w, AView a, uint32_
         const uint8_t* wd = w.dt + kq_tile_off((w.nb + 1) / 2, n0, 0, 4);
         const uint32_t nstage = 4 * nsb;
 
-        // DMA instruction p of stage st (parts past kBase only at a super-block's first stage)
-        // (the LDS addresses are wavefront-uniform; readfirstlane states it
-        // where the group/row specialisation hides it from the compiler)
+        // The LDS addresses are wavefront-uniform; readfirstlane states it
+        // where the row specialisation (PART) hides it from the compiler.
         auto dma16u = [](const void* base, uint32_t off, uint32_t lds_addr) {
             dma16(base, off, PART ? __builtin_amdgcn_readfirstlane(lds_addr) : lds_addr);
         };
         auto dma4u = [](const void* base, uint32_t off, uint32_t lds_addr) {
             dma4(base, off, PART ? __builtin_amdgcn_readfirstlane(lds_addr) : lds_addr);
         };
+        // DMA instruction p of stage st (parts past kBase only at a super-block's first stage)
         auto issue_part = [&](uint32_t st, int p) {
             const uint32_t slot = st % kRing, sb = st >> 2;
             const uint32_t epi = lbase + L::kOffEpi + (sb & 1) * L::kEpi;
