@@ -213,6 +213,24 @@ def test_matmul_prefill_sizes(orc, dev, dt, m, n, k):
     assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("dt,m", [(Q4K, 96), (Q4K, 512), (Q6K, 300), (Q6K, 64)])
+def test_matmul_prefill_long_k(orc, dev, dt, m):
+    """The prefill-sized routes at the down projection's K = 14336 (56
+    super-blocks per row; 4096 -> 14336 is the only K of the config-4
+    prefill shapes): Q4_K on the prefill kernel (at N = 256, 64-row tiles
+    split 28 ways along K), Q6_K on the tiled kernel (300 rows: its
+    half-empty-tail instance, split along K) and on the skinny kernel (64
+    rows), at the auto route."""
+    rng = np.random.default_rng(8200 + dt + m)
+    k, n = 14336, 256
+    blocks = orc.from_float(dt, rng.normal(0, 0.02, (n, k)))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qt = upload(blocks, n, k, dt, dev)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
+    assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} k={k}")
+
+
 @pytest.mark.parametrize("m,n,k", [(4, 301, 2304), (5, 77, 768), (7, 130, 8448), (8, 257, 256), (12, 99, 2304),
                                    (16, 64, 4096)])
 def test_matmul_q4k_multirow_matvec(orc, dev, m, n, k):
