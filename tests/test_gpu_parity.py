@@ -421,9 +421,10 @@ def test_capture_graph_replay(orc, dev):
     q4, g, u, q6 = (upload(b, n, k, dt, dev) for b, dt in ((b4, Q4K), (bg, Q4K), (bu, Q4K), (b6, Q6K)))
     xs = {m: torch.zeros((m, k), dtype=torch.float32, device=dev) for m in (1, 16, 300)}
     ys = {name: torch.zeros((m, n), dtype=torch.float32, device=dev)
-          for name, m in (("mv", 1), ("gate", 1), ("sk", 16), ("mf", 300))}
+          for name, m in (("mv", 1), ("gate", 1), ("sk", 16), ("mf", 300), ("t6", 300))}
     ws16 = torch.empty(max(q6.matmul_t_workspace_size(16), 1), dtype=torch.uint8, device=dev)
     ws300 = torch.empty(max(q4.matmul_t_workspace_size(300), 1), dtype=torch.uint8, device=dev)
+    ws6 = torch.empty(max(q6.matmul_t_workspace_size(300), 1), dtype=torch.uint8, device=dev)
     stream = torch.cuda.Stream(dev)
 
     def run():
@@ -431,6 +432,7 @@ def test_capture_graph_replay(orc, dev):
         matmul_t_silu_gate(g, u, (1, k, n), xs[1], ys["gate"])
         q6.matmul_t_ws((16, k, n), xs[16], ws16, ys["sk"])
         q4.matmul_t_ws((300, k, n), xs[300], ws300, ys["mf"])
+        q6.matmul_t_ws((300, k, n), xs[300], ws6, ys["t6"])  # tiled kernel, half-empty last tile, K split
 
     torch.cuda.synchronize()
     with capture(stream) as c:
@@ -458,6 +460,7 @@ def test_capture_graph_replay(orc, dev):
             assert_close(got["mv"].cpu().numpy(), orc.matmul(Q4K, host[1], b4, n), "captured matvec")
             assert_close(got["sk"].cpu().numpy(), orc.matmul(Q6K, host[16], b6, n), "captured skinny")
             assert_close(got["mf"].cpu().numpy(), orc.matmul(Q4K, host[300], b4, n), "captured prefill")
+            assert_close(got["t6"].cpu().numpy(), orc.matmul(Q6K, host[300], b6, n), "captured tiled")
 
 
 def test_matmul_t_refuses_to_allocate_in_capture(orc, dev):
