@@ -49,3 +49,68 @@ def test_random_shape(orc, dev, dt, m, n, k):
     dst = torch.empty((m, n), dtype=torch.float32, device=dev)
     qt.matmul_t((m, k, n), torch.from_numpy(x).to(dev), dst)
     assert_close(dst.cpu().numpy(), orc.matmul(dt, x, blocks, n), f"dt={dt} m={m} n={n} k={k}")
+
+
+def group_cases(count: int = 24, seed: int = 4242):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        dt = [Q4K, Q6K, Q4_0, Q8_0][i % 4]
+        m = int(M_CHOICES[rng.integers(len(M_CHOICES))])
+        ns = tuple(int(v) for v in rng.integers(1, 400, size=int(rng.integers(1, 4))))
+        k = 256 * int(rng.integers(1, 9))
+        out.append((dt, m, ns, k))
+    return out
+
+
+@pytest.mark.parametrize("dt,m,ns,k", group_cases())
+def test_random_group(orc, dev, dt, m, ns, k):
+    """One to three weights on one activation (llama.rs:156-158), at random
+    rows and widths: the joined matvec or skinny launch, or one shared
+    quantize then a matmul per weight."""
+    from tests.test_gpu_parity import assert_close, upload
+    from xn_amd.quantized import matmul_t_group
+
+    rng = np.random.default_rng(5000 + dt + 11 * m + sum(ns) + k)
+    blocks = [orc.from_float(dt, rng.normal(0, 0.02, (n, k))) for n in ns]
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    qts = [upload(b, n, k, dt, dev) for b, n in zip(blocks, ns)]
+    dsts = [torch.full((m, n), float("nan"), dtype=torch.float32, device=dev) for n in ns]
+    matmul_t_group(qts, m, k, torch.from_numpy(x).to(dev), dsts)
+    for i, (b, n) in enumerate(zip(blocks, ns)):
+        assert_close(dsts[i].cpu().numpy(), orc.matmul(dt, x, b, n), f"group dt={dt} m={m} k={k} weight {i} n={n}")
+
+
+def mlp_cases(count: int = 16, seed: int = 777):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        dt, down_dt = [(Q4K, Q6K), (Q4K, Q4K), (Q6K, Q6K), (Q4_0, Q4_0)][i % 4]
+        m = int(M_CHOICES[rng.integers(len(M_CHOICES))])
+        k = 256 * int(rng.integers(1, 9))
+        f = 256 * int(rng.integers(1, 9))
+        n = int(rng.integers(1, 400))
+        out.append((dt, down_dt, m, k, f, n))
+    return out
+
+
+@pytest.mark.parametrize("dt,down_dt,m,k,f,n", mlp_cases())
+def test_random_mlp(orc, dev, dt, down_dt, m, k, f, n):
+    """The SwiGLU MLP entry (llama.rs:236-264) at random rows and widths: h
+    against the oracle's silu(x . gate) * (x . up), y against the oracle's
+    down projection of the device's h."""
+    from tests.test_gpu_parity import _silu, assert_close, upload
+    from xn_amd.quantized import mlp_t
+
+    rng = np.random.default_rng(6000 + 7 * dt + down_dt + m + k + f + n)
+    gb = orc.from_float(dt, rng.normal(0, 0.02, (f, k)))
+    ub = orc.from_float(dt, rng.normal(0, 0.02, (f, k)))
+    db = orc.from_float(down_dt, rng.normal(0, 0.02, (n, f)))
+    g, u, d = upload(gb, f, k, dt, dev), upload(ub, f, k, dt, dev), upload(db, n, f, down_dt, dev)
+    xh = rng.normal(0, 1, (m, k)).astype(np.float32)
+    h = torch.empty((m, f), dtype=torch.float32, device=dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    mlp_t(g, u, d, m, torch.from_numpy(xh).to(dev), h, y)
+    want_h = _silu(orc.matmul(dt, xh, gb, f).astype(np.float64)) * orc.matmul(dt, xh, ub, f)
+    assert_close(h.cpu().numpy(), want_h, f"mlp h dt={dt} m={m} k={k} f={f}")
+    assert_close(y.cpu().numpy(), orc.matmul(down_dt, h.cpu().numpy(), db, n), f"mlp y dt={dt} m={m} f={f} n={n}")
